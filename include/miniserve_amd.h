@@ -1,0 +1,158 @@
+/*
+ * miniserve_amd -- C ABI of the MI355X (gfx950) kernels for MiniServe's per-step hot path.
+ *
+ * Every entry point takes plain device pointers, sizes and a HIP stream (hipStream_t passed as
+ * void*, NULL = the default stream), launches asynchronously on that stream, allocates nothing,
+ * never synchronizes, and returns MSA_OK or an error code; msa_last_error() then holds a message.
+ * bf16 tensors are passed as uint16_t bit patterns. All tensors are row-major.
+ *
+ * The reference is pure Python + PyTorch (no FFI of its own); each declaration names the
+ * reference function (file:line, paths relative to the reference repository) whose GPU work it
+ * replaces. The Python host mirror in miniserve_amd/ binds these through ctypes.
+ */
+#ifndef MINISERVE_AMD_H
+#define MINISERVE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* msa_stream_t;
+
+enum {
+  MSA_OK = 0,
+  MSA_ERR_INVALID = 1,     /* bad shape, pointer, alignment or argument            */
+  MSA_ERR_UNSUPPORTED = 2, /* valid but not implemented (e.g. head_dim != 128)       */
+  MSA_ERR_LAUNCH = 3,      /* the HIP runtime reported an error for a launch         */
+  MSA_ERR_WORKSPACE = 4    /* workspace missing or smaller than the *_workspace_size */
+};
+
+/* Message of the last failing call on the calling host thread ("" if none). */
+const char* msa_last_error(void);
+/* ABI version: bumped whenever a signature below changes. */
+int msa_abi_version(void);
+
+/* ---- int8 weight-only linears (quant/int8.py) ----------------------------------------------- */
+
+/* Int8Linear.__init__ (quant/int8.py:25-33): per-row scale32 = max(max|w|, 1e-8) / 127 (IEEE
+ * division), qweight = round_half_even(w / scale32) clamped to [-127, 127], scale = bf16(scale32).
+ * weight_dtype: 0 = bf16, 1 = float32. weight [rows, cols], qweight [rows, cols], scale [rows]. */
+int msa_int8_quantize(const void* weight, int weight_dtype, int64_t rows, int64_t cols,
+                      int8_t* qweight, uint16_t* scale, msa_stream_t stream);
+
+enum {
+  MSA_EPI_NONE = 0,     /* y = bf16(x @ W^T)                                                   */
+  MSA_EPI_SILU_MUL = 1, /* rows [gate | up] (layers.py:77-78): y = bf16(silu(g) * u), n/2 cols  */
+  MSA_EPI_RESIDUAL = 2  /* y = bf16(residual + bf16(x @ W^T))  (model/qwen3.py:122)             */
+};
+
+/* Bytes of float32 workspace msa_int8_linear may use for this shape (0 if none). With less (or no)
+ * workspace the call still succeeds, without splitting K across workgroups. */
+size_t msa_int8_linear_workspace_size(int64_t m, int64_t n, int64_t k);
+
+/* Int8Linear.forward (quant/int8.py:35-37) without materializing W: y[m, :] from x [m, k] (row
+ * stride ldx), qweight [n, k] int8, scale [n] bf16. Each weight is dequantized in registers to
+ * bf16(q * s) -- the same value the reference's whole-matrix dequantization produces -- then
+ * multiplied on bf16 MFMA tiles with float32 accumulation. k % 16 == 0; x, qweight 16-byte
+ * aligned. y has n columns (n/2 for MSA_EPI_SILU_MUL) with row stride ldy; residual (row stride
+ * ldr) is read only for MSA_EPI_RESIDUAL and may alias y. When K is split across workgroups the
+ * splits meet in the workspace and a second kernel sums them in a fixed order (deterministic). */
+int msa_int8_linear(const uint16_t* x, int64_t m, int64_t k, int64_t ldx, const int8_t* qweight,
+                    const uint16_t* scale, int64_t n, uint16_t* y, int64_t ldy, int epilogue,
+                    const uint16_t* residual, int64_t ldr, void* workspace, size_t workspace_bytes,
+                    msa_stream_t stream);
+
+/* The split-K half of Int8Linear.forward (quant/int8.py:35-37) for callers that fuse the
+ * reduction into the next kernel: partials[s][m][n] (float32, k_split * m * n elements) holds the
+ * product over the s-th of k_split equal ranges of 64-aligned K chunks (ranges past k hold zeros);
+ * bf16(sum over s in order) is what msa_int8_linear returns. 1 <= k_split <= ceil(k / 64). */
+int msa_int8_linear_splitk(const uint16_t* x, int64_t m, int64_t k, int64_t ldx, const int8_t* qweight,
+                           const uint16_t* scale, int64_t n, int k_split, float* partials,
+                           msa_stream_t stream);
+
+/* ---- norms, RoPE and the KV-cache write (model/layers.py, model/qwen3.py) -------------------- */
+
+/* RMSNorm.forward (model/layers.py:18-22): out = bf16(w * bf16(x * rsqrt(mean(x^2) + eps))). */
+int msa_rmsnorm(const uint16_t* x, int64_t ldx, const uint16_t* weight, uint16_t* out, int64_t ldo,
+                int64_t rows, int64_t dim, float eps, msa_stream_t stream);
+
+/* The residual add then RMSNorm of Qwen3DecoderLayer.forward (model/qwen3.py:121-122):
+ * residual_out = bf16(residual + delta) (residual_out may alias residual), out =
+ * RMSNorm(residual_out). Rows are contiguous [rows, dim]. */
+int msa_add_rmsnorm(const uint16_t* residual, const uint16_t* delta, uint16_t* residual_out,
+                    const uint16_t* weight, uint16_t* out, int64_t rows, int64_t dim, float eps,
+                    msa_stream_t stream);
+
+/* msa_add_rmsnorm whose delta is the bf16 sum of k_split float32 partials [k_split][rows][dim]
+ * from msa_int8_linear_splitk -- the o_proj / down_proj output, residual add and the following
+ * RMSNorm of Qwen3DecoderLayer.forward (model/qwen3.py:121-122) in one kernel. dim % 4 == 0. */
+int msa_splitk_add_rmsnorm(const float* partials, int k_split, const uint16_t* residual,
+                           uint16_t* residual_out, const uint16_t* weight, uint16_t* out, int64_t rows,
+                           int64_t dim, float eps, msa_stream_t stream);
+
+/* Qwen3Attention.forward after qkv_proj (model/qwen3.py:94-98) plus the cache write of
+ * paged_attention (attention/backends.py:159-160): split qkv [tokens, (H + 2 KVH) * D] (row stride
+ * ldqkv) into q | k | v; per-head RMSNorm of q and k with q_norm_w / k_norm_w [D]; RoPE with the
+ * float32 rows cos, sin [tokens, D] (cast to bf16 as layers.py:63-64 does); q -> q_out [tokens,
+ * H, D]; k, v -> k_cache, v_cache [num_slots, KVH, D] at slot_mapping[t]. Slots outside
+ * [0, num_slots) are not written. D even, D <= 256. */
+int msa_qk_norm_rope_cache(const uint16_t* qkv, int64_t ldqkv, int64_t tokens, int heads, int kv_heads,
+                           int head_dim, const uint16_t* q_norm_w, const uint16_t* k_norm_w, float eps,
+                           const float* cos, const float* sin, const int64_t* slot_mapping,
+                           uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache, int64_t num_slots,
+                           msa_stream_t stream);
+
+/* msa_qk_norm_rope_cache reading the qkv rows as k_split float32 partials
+ * [k_split][tokens][(H + 2 KVH) * D] from msa_int8_linear_splitk (summed in order, rounded to bf16). */
+int msa_qk_norm_rope_cache_splitk(const float* partials, int k_split, int64_t tokens, int heads, int kv_heads,
+                                  int head_dim, const uint16_t* q_norm_w, const uint16_t* k_norm_w, float eps,
+                                  const float* cos, const float* sin, const int64_t* slot_mapping,
+                                  uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache, int64_t num_slots,
+                                  msa_stream_t stream);
+
+/* k_cache.index_copy_(0, slot_mapping, k) and the same for v (attention/backends.py:159-160).
+ * k, v [tokens, KVH, D] with row strides ldk, ldv (elements per token). */
+int msa_reshape_and_cache(const uint16_t* k, int64_t ldk, const uint16_t* v, int64_t ldv, int64_t tokens,
+                          int kv_heads, int head_dim, const int64_t* slot_mapping, uint16_t* k_cache,
+                          uint16_t* v_cache, int64_t num_slots, msa_stream_t stream);
+
+/* ---- paged attention (attention/backends.py:145-197) ----------------------------------------- */
+
+size_t msa_paged_attention_decode_workspace_size(int num_seqs, int heads, int head_dim, int max_partitions);
+
+/* The batched short-query path of paged_attention (attention/backends.py:165-180) for one new
+ * token per sequence, reading K/V blocks in place instead of gathering them: sequence i's query
+ * is row q_rows[i] of q [*, H, D] (row stride ldq), its keys are positions 0..context_lens[i]-1
+ * through block_tables[i, :] (int32, row stride max_blocks), query head h reads KV head
+ * h / (H / KVH); out row q_rows[i] (row stride ldo). A workgroup of wavefronts covers
+ * partition_tokens keys of one (sequence, KV head) with an online softmax; with max_partitions > 1
+ * the partitions meet in the workspace (msa_paged_attention_decode_workspace_size bytes) and a
+ * second kernel merges them. partition_tokens % 16 == 0 and partition_tokens * max_partitions >=
+ * 16 * max_blocks. D == 128, block_size == 16, H / KVH in {1, 2, 4, 8}. */
+int msa_paged_attention_decode(const uint16_t* q, int64_t ldq, const uint16_t* k_cache,
+                               const uint16_t* v_cache, int64_t num_slots, int heads, int kv_heads,
+                               int head_dim, int block_size, const int32_t* block_tables, int max_blocks,
+                               const int32_t* context_lens, const int32_t* q_rows, int num_seqs,
+                               int partition_tokens, int max_partitions, float scale, uint16_t* out,
+                               int64_t ldo, void* workspace, size_t workspace_bytes, msa_stream_t stream);
+
+/* The prefill path of paged_attention (attention/backends.py:182-196) for chunks of any length,
+ * fresh or continuing from cached keys: causal attention of each new token over positions
+ * 0..its own, keys and values read through the block table from the caches (which already hold
+ * this step's tokens). seq_info [num_seqs, 3] int32 = (first flat row, num_new, num_cached);
+ * work [num_work, 2] int32 = (sequence index, first new-token index of a 64 / (H / KVH)-token
+ * tile). D == 128, block_size == 16, H / KVH in {1, 2, 4}. */
+int msa_paged_attention_prefill(const uint16_t* q, int64_t ldq, const uint16_t* k_cache,
+                                const uint16_t* v_cache, int64_t num_slots, int heads, int kv_heads,
+                                int head_dim, int block_size, const int32_t* block_tables, int max_blocks,
+                                const int32_t* seq_info, const int32_t* work, int num_work, float scale,
+                                uint16_t* out, int64_t ldo, msa_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MINISERVE_AMD_H */

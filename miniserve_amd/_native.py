@@ -1,0 +1,115 @@
+"""ctypes binding of the C ABI in ``include/miniserve_amd.h`` (``libminiserve_amd.so``).
+
+The library is loaded once, after ``torch`` (so that the process holds a single HIP runtime:
+torch's ``libamdhip64``), and every call goes through :func:`call`, which raises
+``RuntimeError`` with the library's message when an entry point fails. There is no fallback: if
+the library is missing or was built against another HIP runtime, loading fails loudly.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from ctypes import c_float, c_int, c_int64, c_size_t, c_void_p
+from pathlib import Path
+
+import torch  # noqa: F401  -- must be imported before the HIP library is loaded
+
+LIB_PATH = Path(__file__).resolve().parent / "libminiserve_amd.so"
+ABI_VERSION = 2
+
+# name -> (restype, argtypes); mirrors include/miniserve_amd.h.
+SIGNATURES: dict[str, tuple[object, list[object]]] = {
+    "msa_last_error": (ctypes.c_char_p, []),
+    "msa_abi_version": (c_int, []),
+    "msa_int8_quantize": (c_int, [c_void_p, c_int, c_int64, c_int64, c_void_p, c_void_p, c_void_p]),
+    "msa_int8_linear_workspace_size": (c_size_t, [c_int64, c_int64, c_int64]),
+    "msa_int8_linear": (
+        c_int,
+        [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_int,
+         c_void_p, c_int64, c_void_p, c_size_t, c_void_p],
+    ),
+    "msa_int8_linear_splitk": (
+        c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int, c_void_p, c_void_p]
+    ),
+    "msa_splitk_add_rmsnorm": (
+        c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_float, c_void_p]
+    ),
+    "msa_qk_norm_rope_cache_splitk": (
+        c_int,
+        [c_void_p, c_int, c_int64, c_int, c_int, c_int, c_void_p, c_void_p, c_float, c_void_p, c_void_p,
+         c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p],
+    ),
+    "msa_rmsnorm": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_float, c_void_p]),
+    "msa_add_rmsnorm": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_float, c_void_p]),
+    "msa_qk_norm_rope_cache": (
+        c_int,
+        [c_void_p, c_int64, c_int64, c_int, c_int, c_int, c_void_p, c_void_p, c_float, c_void_p, c_void_p,
+         c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p],
+    ),
+    "msa_reshape_and_cache": (
+        c_int,
+        [c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int, c_int, c_void_p, c_void_p, c_void_p, c_int64, c_void_p],
+    ),
+    "msa_paged_attention_decode_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int]),
+    "msa_paged_attention_decode": (
+        c_int,
+        [c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int, c_int, c_int, c_int, c_void_p, c_int, c_void_p,
+         c_void_p, c_int, c_int, c_int, c_float, c_void_p, c_int64, c_void_p, c_size_t, c_void_p],
+    ),
+    "msa_paged_attention_prefill": (
+        c_int,
+        [c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int, c_int, c_int, c_int, c_void_p, c_int, c_void_p,
+         c_void_p, c_int, c_float, c_void_p, c_int64, c_void_p],
+    ),
+}
+
+_lib: ctypes.CDLL | None = None
+_lock = threading.Lock()
+
+
+def _hip_runtimes_mapped() -> set[str]:
+    try:
+        with open("/proc/self/maps") as f:
+            return {line.split()[-1] for line in f if "libamdhip64" in line}
+    except OSError:
+        return set()
+
+
+def load() -> ctypes.CDLL:
+    """Load and bind the library (idempotent). Raises RuntimeError if it cannot be used."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python -m miniserve_amd.build` "
+                "(there is no fallback path)"
+            )
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, (restype, argtypes) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        if lib.msa_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"{LIB_PATH} has ABI {lib.msa_abi_version()}, expected {ABI_VERSION}: rebuild it")
+        runtimes = _hip_runtimes_mapped()
+        if len(runtimes) > 1:
+            raise RuntimeError(f"two HIP runtimes are mapped into this process: {sorted(runtimes)}")
+        _lib = lib
+        return lib
+
+
+def call(name: str, *args: object) -> None:
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        msg = lib.msa_last_error().decode(errors="replace")
+        raise RuntimeError(f"{name} failed ({rc}): {msg}")
+
+
+def query(name: str, *args: object) -> int:
+    return int(getattr(load(), name)(*args))

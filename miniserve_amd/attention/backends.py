@@ -1,0 +1,178 @@
+"""Paged attention over a slot pool, read in place by HIP kernels (reference:
+src/miniserve/attention/backends.py).
+
+Per layer the pool is ``[num_slots, kv_heads, head_dim]`` with slot = block * block_size + offset.
+Each step (backends.py:145-197): write the new tokens' keys/values at ``slot_mapping``, then every
+new token attends to positions 0..its own through its sequence's block table.
+
+What differs from the reference is the plan, not the result: instead of gathering each sequence's
+keys into contiguous tensors and padding groups for SDPA, ``build_attention_metadata`` prepares
+int32 block tables and per-sequence lengths (one pinned, non-blocking upload per step) and the
+kernels read the blocks where they lie:
+  * sequences with one new token (decodes) -> split-K decode kernel;
+  * sequences with more (prefill chunks, fresh or after cached keys, speculative verifies) ->
+    the flash-style MFMA prefill kernel.
+The metadata is built once per step and shared by all layers (backends.py:19-20).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+from torch import Tensor
+
+from miniserve_amd import kernels
+from miniserve_amd.utils import upload_int32
+
+SHORT_QUERY = 8  # the reference's batched-path threshold (backends.py:32); kept for callers
+MAX_GATHER_TOKENS = 16384  # the reference's gather cap (backends.py:33); nothing is gathered here
+PREFILL_TILES = (64, 32, 16)  # query tokens per prefill workgroup for H/KVH = 1, 2, 4
+
+
+@dataclass
+class SeqChunk:
+    """What attention needs to know about one scheduled sequence (backends.py:36-47)."""
+
+    flat_start: int
+    num_new: int
+    num_cached: int
+    block_table: list[int]
+
+    @property
+    def context_len(self) -> int:
+        return self.num_cached + self.num_new
+
+
+@dataclass
+class DecodePlan:
+    q_rows: Tensor  # [B] int32 flat-batch row of each sequence's query
+    context_lens: Tensor  # [B] int32
+    block_tables: Tensor  # [B, max_blocks] int32, padded with block 0
+
+    @property
+    def num_seqs(self) -> int:
+        return int(self.q_rows.numel())
+
+
+@dataclass
+class PrefillPlan:
+    seq_info: Tensor  # [S, 3] int32: flat start, num_new, num_cached
+    block_tables: Tensor  # [S, max_blocks] int32
+    work: dict[int, Tensor] = field(default_factory=dict)  # tile tokens -> [W, 2] int32
+
+
+@dataclass
+class AttentionMetadata:
+    slot_mapping: Tensor  # [T] int64 slot where each new token's K/V is written
+    block_size: int
+    decode: DecodePlan | None
+    prefill: PrefillPlan | None
+
+
+def context_slots(block_tables: Tensor, length: int, block_size: int) -> Tensor:
+    """Slot of positions 0..length-1 through a block table (backends.py:74-77)."""
+    pos = torch.arange(length, device=block_tables.device)
+    return block_tables[..., pos // block_size] * block_size + pos % block_size
+
+
+def _cdiv(a: int, b: int) -> int:
+    return -(-a // b)
+
+
+def build_attention_metadata(chunks: list[SeqChunk], slot_mapping: Tensor, block_size: int) -> AttentionMetadata:
+    """Plan one step's attention (backends.py:80-98): one int32 upload holds every table."""
+    if block_size != 16:
+        raise RuntimeError("the HIP attention kernels use 16-token blocks")
+    device = slot_mapping.device
+    dec = [c for c in chunks if c.num_new == 1]
+    pre = [c for c in chunks if c.num_new > 1]
+    parts: list[np.ndarray] = []
+    layout: list[tuple[str, tuple[int, ...]]] = []
+
+    def add(name: str, arr: np.ndarray) -> None:
+        parts.append(np.ascontiguousarray(arr, dtype=np.int32).ravel())
+        layout.append((name, arr.shape))
+
+    if dec:
+        nb = max(_cdiv(c.context_len, block_size) for c in dec)
+        tables = np.zeros((len(dec), nb), dtype=np.int32)
+        for i, c in enumerate(dec):
+            need = _cdiv(c.context_len, block_size)
+            if len(c.block_table) < need:
+                raise RuntimeError(f"block table of {len(c.block_table)} blocks is shorter than context {c.context_len}")
+            tables[i, :need] = c.block_table[:need]
+        ctx = np.array([c.context_len for c in dec], dtype=np.int32)
+        add("d_rows", np.array([c.flat_start for c in dec], dtype=np.int32))
+        add("d_ctx", ctx)
+        add("d_tables", tables)
+    if pre:
+        nb = max(_cdiv(c.context_len, block_size) for c in pre)
+        tables = np.zeros((len(pre), nb), dtype=np.int32)
+        for i, c in enumerate(pre):
+            need = _cdiv(c.context_len, block_size)
+            if len(c.block_table) < need:
+                raise RuntimeError(f"block table of {len(c.block_table)} blocks is shorter than context {c.context_len}")
+            tables[i, :need] = c.block_table[:need]
+        add("p_info", np.array([[c.flat_start, c.num_new, c.num_cached] for c in pre], dtype=np.int32))
+        add("p_tables", tables)
+        for tile in PREFILL_TILES:
+            work = [(i, t0) for i, c in enumerate(pre) for t0 in range(0, c.num_new, tile)]
+            add(f"p_work{tile}", np.array(work, dtype=np.int32).reshape(-1, 2))
+
+    views: dict[str, Tensor] = {}
+    if parts:
+        flat = upload_int32(np.concatenate(parts), device)
+        off = 0
+        for (name, shape), arr in zip(layout, parts, strict=True):
+            views[name] = flat[off : off + arr.size].view(*shape)
+            off += arr.size
+    decode = (
+        DecodePlan(views["d_rows"], views["d_ctx"], views["d_tables"]) if dec else None
+    )
+    prefill = (
+        PrefillPlan(views["p_info"], views["p_tables"], {t: views[f"p_work{t}"] for t in PREFILL_TILES})
+        if pre
+        else None
+    )
+    return AttentionMetadata(slot_mapping, block_size, decode, prefill)
+
+
+def attend(q: Tensor, k_cache: Tensor, v_cache: Tensor, meta: AttentionMetadata, scale: float) -> Tensor:
+    """Attention of every new token over its cached context (the caches already hold this
+    step's keys and values). q [T, H, D] -> [T, H, D]."""
+    out = torch.empty_like(q)
+    heads, kv_heads = q.shape[1], k_cache.shape[1]
+    if meta.decode is not None:
+        d = meta.decode
+        ptok, parts = kernels.decode_splits(d.num_seqs, kv_heads, d.block_tables.shape[1])
+        kernels.paged_attention_decode(
+            q, k_cache, v_cache, d.block_tables, d.context_lens, d.q_rows, ptok, parts, scale, out, meta.block_size
+        )
+    if meta.prefill is not None:
+        p = meta.prefill
+        group = heads // kv_heads
+        tile = {1: 64, 2: 32, 4: 16}.get(group)
+        if tile is None:
+            raise RuntimeError(f"prefill attention supports H/KVH in 1, 2, 4 (got {group})")
+        kernels.paged_attention_prefill(q, k_cache, v_cache, p.block_tables, p.seq_info, p.work[tile], scale, out,
+                                        meta.block_size)
+    return out
+
+
+def paged_attention(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    k_cache: Tensor,
+    v_cache: Tensor,
+    meta: AttentionMetadata,
+    scale: float,
+) -> Tensor:
+    """Write this step's keys and values into the cache, then attend through it (backends.py:145-197).
+
+    q: [T, heads, dim]; k, v: [T, kv_heads, dim]; caches: [slots, kv_heads, dim]. Returns [T, heads, dim].
+    """
+    kernels.reshape_and_cache(k, v, k_cache, v_cache, meta.slot_mapping)
+    return attend(q, k_cache, v_cache, meta, scale)

@@ -1,0 +1,484 @@
+// Paged attention over the slot pool [num_slots, KVH, D] (slot = block * 16 + offset), GQA with
+// query head h reading KV head h / (H / KVH), scale applied to q.k, softmax over the visible keys.
+//
+// Decode (one new token per sequence): a workgroup of eight wavefronts per (sequence, KV head);
+// the wavefronts interleave the sequence's 16-token blocks. A 256-byte key/value row (128 bf16) is
+// read by 16 lanes with 16-byte loads, four token rows per load instruction, straight from the
+// pool through the block table -- no gathered copy. The G = H / KVH query heads of the KV head
+// share every K/V load. Dot products are float32 FMAs reduced over the 16 lanes with DPP; the
+// online softmax keeps (max, sum, acc) per lane, merges the four token rows at the end, then the
+// wavefronts through LDS. Only when sequences x KV heads are too few to fill the GPU does the host
+// add workgroup-level splits; those write (acc, max, sum) to a workspace and a second small
+// kernel merges them -- no workgroup ever waits for another.
+//
+// Prefill (any number of new tokens, fresh or after cached keys): flash-attention on MFMA. A
+// workgroup of four wavefronts owns one KV head and 64 / G query tokens; wavefront w takes query
+// head w % G and 16 of the tokens. Per 32-key tile the workgroup stages K (row-major) and V
+// (transposed) in LDS, then each wavefront computes S^T = K Q^T (v_mfma_f32_16x16x32_bf16, 2 x 4
+// instructions) so each lane holds 8 scores of ONE query, applies the causal mask and an online
+// softmax with lane-local statistics, and accumulates O^T += V^T P^T (8 instructions) with P in
+// bf16.
+#include "common.h"
+
+namespace msa {
+
+constexpr int kHeadDim = 128;
+constexpr int kBlock = 16;
+
+struct DecodeArgs {
+  const uint16_t* q;
+  int64_t ldq;
+  const uint16_t* kc;
+  const uint16_t* vc;
+  int64_t num_blocks;
+  int heads;
+  int kv_heads;
+  const int32_t* bt;
+  int max_blocks;
+  const int32_t* ctx;
+  const int32_t* qrows;
+  int part_tokens;  // keys per workgroup-level split (multiple of 16)
+  int splits;       // workgroups per (sequence, KV head)
+  float scale_log2;
+  uint16_t* out;
+  int64_t ldo;
+  float* ws_o;   // [num_seqs][heads][splits][128] unnormalized output of each split
+  float* ws_ml;  // [num_seqs][heads][splits][2]   (running max, sum of exp) of each split
+};
+
+__device__ __forceinline__ void unpack8(const uint4& v, float (&f)[8]) {
+  f[0] = bf16lo(v.x); f[1] = bf16hi(v.x);
+  f[2] = bf16lo(v.y); f[3] = bf16hi(v.y);
+  f[4] = bf16lo(v.z); f[5] = bf16hi(v.z);
+  f[6] = bf16lo(v.w); f[7] = bf16hi(v.w);
+}
+
+// Keys a sequence may read: its context, clamped to its block-table row (memory safety when a
+// caller passes inconsistent sizes; correct calls never hit the clamp).
+__device__ __forceinline__ int decode_context(const DecodeArgs& a, int seq) {
+  const int ctx = a.ctx[seq];
+  const int cap = a.max_blocks * kBlock;
+  return ctx < cap ? ctx : cap;
+}
+
+// Workgroup = W wavefronts for one (sequence, KV head, split). Wave w takes blocks b0 + w,
+// b0 + w + W, ... of the split, keeping one block of K and V in flight ahead of the one it
+// computes. Lane (r, c) = (lane / 16, lane % 16) owns dims 8c..8c+7 of token rows r, r+4, r+8,
+// r+12 of each block. The waves meet in LDS at the end.
+template <int G, int W>
+__global__ __launch_bounds__(64 * W) void paged_decode_kernel(DecodeArgs a) {
+  __shared__ float s_acc[W][G][kHeadDim];
+  __shared__ float s_ml[W][G][2];
+  const int split = blockIdx.x, seq = blockIdx.y, kvh = blockIdx.z;
+  const int ctx = decode_context(a, seq);
+  const int start = split * a.part_tokens;
+  if (start >= ctx) return;  // the reduce kernel merges only splits that hold keys
+  const int end = min(ctx, start + a.part_tokens);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane >> 4, c = lane & 15;
+  const int64_t qrow = a.qrows[seq];
+
+  float qf[G][8];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    const uint4 v = *(const uint4*)(a.q + qrow * a.ldq + (int64_t)(kvh * G + h) * kHeadDim + c * 8);
+    unpack8(v, qf[h]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qf[h][e] *= a.scale_log2;
+  }
+  float m[G], l[G], acc[G][8];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    m[h] = -INFINITY;
+    l[h] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
+  }
+
+  const int b1 = (end + kBlock - 1) / kBlock;
+  const int32_t* btr = a.bt + (int64_t)seq * a.max_blocks;
+  const int64_t tok_stride = (int64_t)a.kv_heads * kHeadDim;
+  const int64_t lane_off = (int64_t)r * tok_stride + (int64_t)kvh * kHeadDim + c * 8;
+  auto block_ptr = [&](int b) -> int64_t {
+    int phys = btr[b];
+    phys = ((uint32_t)phys < (uint64_t)a.num_blocks) ? phys : 0;  // out-of-range table entries read block 0
+    return (int64_t)phys * kBlock * tok_stride + lane_off;
+  };
+
+  int b = start / kBlock + wave;
+  uint4 kv[4], vv[4];
+  if (b < b1) {
+    const int64_t base = block_ptr(b);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      kv[i] = *(const uint4*)(a.kc + base + 4 * i * tok_stride);
+      vv[i] = *(const uint4*)(a.vc + base + 4 * i * tok_stride);
+    }
+  }
+  for (; b < b1; b += W) {
+    uint4 kn[4], vn[4];
+    const bool more = b + W < b1;
+    if (more) {
+      const int64_t base = block_ptr(b + W);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        kn[i] = *(const uint4*)(a.kc + base + 4 * i * tok_stride);
+        vn[i] = *(const uint4*)(a.vc + base + 4 * i * tok_stride);
+      }
+    }
+    float s[G][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float kf[8];
+      unpack8(kv[i], kf);
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        float d = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) d = fmaf(qf[h][e], kf[e], d);
+        s[h][i] = row16_sum(d);
+      }
+      if (b * kBlock + 4 * i + r >= end) {
+#pragma unroll
+        for (int h = 0; h < G; ++h) s[h][i] = -INFINITY;
+        vv[i] = uint4{0, 0, 0, 0};  // masked rows contribute exactly zero even if stale
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      float bm = fmaxf(fmaxf(s[h][0], s[h][1]), fmaxf(s[h][2], s[h][3]));
+      bm = xrow_max(bm);  // every block holds at least one visible key
+      const float mn = fmaxf(m[h], bm);
+      const float alpha = exp2f(m[h] - mn);
+      m[h] = mn;
+      l[h] *= alpha;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[h][e] *= alpha;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        s[h][i] = exp2f(s[h][i] - mn);
+        l[h] += s[h][i];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float vf[8];
+      unpack8(vv[i], vf);
+#pragma unroll
+      for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(s[h][i], vf[e], acc[h][e]);
+    }
+    if (more) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        kv[i] = kn[i];
+        vv[i] = vn[i];
+      }
+    }
+  }
+  // Merge the four token rows of the wavefront, then the wavefronts through LDS.
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    l[h] = xrow_sum(l[h]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[h][e] = xrow_sum(acc[h][e]);
+    if (r == 0) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s_acc[wave][h][c * 8 + e] = acc[h][e];
+    }
+    if (lane == 0) {
+      s_ml[wave][h][0] = m[h];  // -inf for a wavefront that got no block
+      s_ml[wave][h][1] = l[h];
+    }
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < G * kHeadDim; idx += 64 * W) {
+    const int h = idx / kHeadDim, d = idx % kHeadDim;
+    float mx = s_ml[0][h][0];  // wavefront 0 always holds the split's first block
+#pragma unroll
+    for (int w = 1; w < W; ++w) mx = fmaxf(mx, s_ml[w][h][0]);
+    float den = 0.f, num = 0.f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      const float f = exp2f(s_ml[w][h][0] - mx);
+      den += f * s_ml[w][h][1];
+      num += f * s_acc[w][h][d];
+    }
+    const int head = kvh * G + h;
+    if (a.splits == 1) {
+      a.out[qrow * a.ldo + (int64_t)head * kHeadDim + d] = f32_to_bf16(num / den);
+    } else {
+      const int64_t slot = ((int64_t)seq * a.heads + head) * a.splits + split;
+      a.ws_o[slot * kHeadDim + d] = num;
+      if (d == 0) *(float2*)(a.ws_ml + slot * 2) = float2{mx, den};
+    }
+  }
+}
+
+// Merge of the workgroup-level splits of each (sequence, query head): one thread per dim.
+__global__ __launch_bounds__(kHeadDim) void paged_decode_reduce_kernel(DecodeArgs a) {
+  const int seq = blockIdx.x, head = blockIdx.y, d = threadIdx.x;
+  const int ctx = decode_context(a, seq);
+  const int nsplit = min(a.splits, (ctx + a.part_tokens - 1) / a.part_tokens);
+  if (nsplit <= 0) return;
+  const int64_t base = ((int64_t)seq * a.heads + head) * a.splits;
+  float mx = -INFINITY;
+  for (int p = 0; p < nsplit; ++p) mx = fmaxf(mx, a.ws_ml[(base + p) * 2]);
+  float den = 0.f, num = 0.f;
+  for (int p = 0; p < nsplit; ++p) {
+    const float2 ml = *(const float2*)(a.ws_ml + (base + p) * 2);
+    const float f = exp2f(ml.x - mx);
+    den += f * ml.y;
+    num += f * a.ws_o[(base + p) * kHeadDim + d];
+  }
+  a.out[(int64_t)a.qrows[seq] * a.ldo + (int64_t)head * kHeadDim + d] = f32_to_bf16(num / den);
+}
+
+// ---------------------------------------------------------------------------------------------
+
+constexpr int kKeyTile = 32;
+constexpr int kKsStride = kHeadDim + 8;  // bf16 elements per K row in LDS
+constexpr int kVtStride = kKeyTile + 4;  // bf16 elements per transposed V row in LDS
+
+struct PrefillArgs {
+  const uint16_t* q;
+  int64_t ldq;
+  const uint16_t* kc;
+  const uint16_t* vc;
+  int64_t num_blocks;
+  int heads;
+  int kv_heads;
+  const int32_t* bt;
+  int max_blocks;
+  const int32_t* seq_info;  // [S][3] flat start, num_new, num_cached
+  const int32_t* work;      // [W][2] sequence, first new-token index of the tile
+  float scale_log2;
+  uint16_t* out;
+  int64_t ldo;
+};
+
+__device__ __forceinline__ uint16_t elem16(const uint4& v, int e) {
+  const uint32_t w = e < 2 ? v.x : e < 4 ? v.y : e < 6 ? v.z : v.w;
+  return (uint16_t)((e & 1) ? (w >> 16) : (w & 0xffff));
+}
+
+template <int G>
+__global__ __launch_bounds__(256) void paged_prefill_kernel(PrefillArgs a) {
+  constexpr int kSub = 4 / G;       // 16-token query sub-tiles per workgroup
+  constexpr int kQTok = 16 * kSub;  // query tokens per workgroup
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[kKeyTile * kKsStride];
+  __shared__ __attribute__((aligned(16))) uint16_t Vt[kHeadDim * kVtStride];
+
+  const int wi = blockIdx.x, kvh = blockIdx.y;
+  const int seq = a.work[2 * wi], tstart = a.work[2 * wi + 1];
+  const int flat = a.seq_info[3 * seq], nnew = a.seq_info[3 * seq + 1], ncached = a.seq_info[3 * seq + 2];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = wave % G, st = wave / G;
+  const int head = kvh * G + g;
+  const int j = lane & 15, grp = lane >> 4;
+
+  const int qi = tstart + st * 16 + j;
+  const bool qvalid = qi < nnew;
+  const int qi_c = qvalid ? qi : nnew - 1;
+  const int qpos = ncached + qi_c;
+  const int wave_last = ncached + min(tstart + st * 16 + 15, nnew - 1);
+
+  bf16x8 qfrag[4];
+  {
+    const uint16_t* qp = a.q + (int64_t)(flat + qi_c) * a.ldq + (int64_t)head * kHeadDim + 8 * grp;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) qfrag[ks] = *(const bf16x8*)(qp + 32 * ks);
+  }
+
+  const int kend = ncached + min(tstart + kQTok, nnew);
+  const int ntiles = (kend + kKeyTile - 1) / kKeyTile;
+  const int32_t* btr = a.bt + (int64_t)seq * a.max_blocks;
+  const int64_t tok_stride = (int64_t)a.kv_heads * kHeadDim;
+
+  // Loader role: key pair la (keys 2la, 2la+1 of the tile), 8-wide dim chunk lb.
+  const int la = lane & 15, lb = wave * 4 + (lane >> 4);
+  uint4 kr[2], vr[2];
+  auto load_tile = [&](int tile) {
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+      const int key = tile * kKeyTile + 2 * la + rr;
+      if (key < kend && key / kBlock < a.max_blocks) {
+        int phys = btr[key / kBlock];
+        phys = ((uint32_t)phys < (uint64_t)a.num_blocks) ? phys : 0;
+        const int64_t off = ((int64_t)phys * kBlock + key % kBlock) * tok_stride + (int64_t)kvh * kHeadDim + 8 * lb;
+        kr[rr] = *(const uint4*)(a.kc + off);
+        vr[rr] = *(const uint4*)(a.vc + off);
+      } else {
+        kr[rr] = uint4{0, 0, 0, 0};
+        vr[rr] = uint4{0, 0, 0, 0};
+      }
+    }
+  };
+
+  f32x4 acc[8];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, l = 0.f;
+
+  load_tile(0);
+  for (int tile = 0; tile < ntiles; ++tile) {
+    __syncthreads();
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) *(uint4*)&Ks[(2 * la + rr) * kKsStride + 8 * lb] = kr[rr];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      *(uint32_t*)&Vt[(8 * lb + e) * kVtStride + 2 * la] = (uint32_t)elem16(vr[0], e) | ((uint32_t)elem16(vr[1], e) << 16);
+    __syncthreads();
+    if (tile + 1 < ntiles) load_tile(tile + 1);
+
+    const int key0 = tile * kKeyTile;
+    if (key0 > wave_last) continue;  // every query of this wavefront precedes the tile
+
+    f32x4 sT[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const bf16x8 kf = *(const bf16x8*)&Ks[(mt * 16 + j) * kKsStride + 32 * ks + 8 * grp];
+        sT[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qfrag[ks], sT[mt], 0, 0, 0);
+      }
+    float s[8];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int key = key0 + mt * 16 + 4 * grp + rr;
+        s[mt * 4 + rr] = key <= qpos ? sT[mt][rr] * a.scale_log2 : -INFINITY;
+      }
+    float bm = s[0];
+#pragma unroll
+    for (int e = 1; e < 8; ++e) bm = fmaxf(bm, s[e]);
+    bm = xrow_max(bm);
+    const float mn = fmaxf(m, bm);  // finite: key 0 is visible to every query
+    const float alpha = exp2f(m - mn);
+    m = mn;
+    l *= alpha;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
+    bf16x8 pb;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float p = exp2f(s[e] - mn);
+      l += p;
+      pb[e] = (__bf16)p;
+    }
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const uint2 v0 = *(const uint2*)&Vt[(dt * 16 + j) * kVtStride + 4 * grp];
+      const uint2 v1 = *(const uint2*)&Vt[(dt * 16 + j) * kVtStride + 16 + 4 * grp];
+      const bf16x8 va = __builtin_bit_cast(bf16x8, uint4{v0.x, v0.y, v1.x, v1.y});
+      acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb, acc[dt], 0, 0, 0);
+    }
+  }
+  l = xrow_sum(l);
+  if (!qvalid) return;
+  const float inv = 1.0f / l;
+  uint16_t* orow = a.out + (int64_t)(flat + qi) * a.ldo + (int64_t)head * kHeadDim;
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) {
+    const int d = dt * 16 + 4 * grp;
+    *(uint2*)(orow + d) = uint2{pack_bf16x2(acc[dt][0] * inv, acc[dt][1] * inv), pack_bf16x2(acc[dt][2] * inv, acc[dt][3] * inv)};
+  }
+}
+
+}  // namespace msa
+
+extern "C" size_t msa_paged_attention_decode_workspace_size(int num_seqs, int heads, int head_dim, int max_partitions) {
+  if (num_seqs <= 0 || heads <= 0 || head_dim <= 0 || max_partitions <= 1) return 0;
+  const size_t slots = (size_t)num_seqs * heads * max_partitions;
+  return slots * head_dim * sizeof(float) + slots * 2 * sizeof(float);
+}
+
+namespace msa {
+template <int G>
+static void launch_decode(const DecodeArgs& a, int num_seqs, hipStream_t s) {
+  // Eight wavefronts per workgroup; four when eight query heads' state would not fit.
+  constexpr int W = G >= 8 ? 4 : 8;
+  const dim3 grid(a.splits, num_seqs, a.kv_heads);
+  hipLaunchKernelGGL((paged_decode_kernel<G, W>), grid, dim3(64 * W), 0, s, a);
+}
+}  // namespace msa
+
+extern "C" int msa_paged_attention_decode(const uint16_t* q, int64_t ldq, const uint16_t* k_cache, const uint16_t* v_cache,
+                                          int64_t num_slots, int heads, int kv_heads, int head_dim, int block_size,
+                                          const int32_t* block_tables, int max_blocks, const int32_t* context_lens,
+                                          const int32_t* q_rows, int num_seqs, int partition_tokens, int max_partitions,
+                                          float scale, uint16_t* out, int64_t ldo, void* workspace,
+                                          size_t workspace_bytes, msa_stream_t stream) {
+  using namespace msa;
+  if (num_seqs == 0) return MSA_OK;
+  if (!q || !k_cache || !v_cache || !block_tables || !context_lens || !q_rows || !out)
+    return fail(MSA_ERR_INVALID, "msa_paged_attention_decode: null pointer");
+  if (head_dim != kHeadDim) return fail(MSA_ERR_UNSUPPORTED, "msa_paged_attention_decode: head_dim must be 128");
+  if (block_size != kBlock) return fail(MSA_ERR_UNSUPPORTED, "msa_paged_attention_decode: block_size must be 16");
+  if (num_seqs < 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads != 0 || max_blocks <= 0)
+    return fail(MSA_ERR_INVALID, "msa_paged_attention_decode: bad shape");
+  if (partition_tokens <= 0 || partition_tokens % kBlock != 0 || max_partitions <= 0 || max_partitions > 65535)
+    return fail(MSA_ERR_INVALID, "msa_paged_attention_decode: partition_tokens must be a positive multiple of 16");
+  if ((int64_t)partition_tokens * max_partitions < (int64_t)max_blocks * kBlock)
+    return fail(MSA_ERR_INVALID, "msa_paged_attention_decode: partition_tokens * max_partitions must cover max_blocks * 16");
+  if (ldq % 8 != 0 || !aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out))
+    return fail(MSA_ERR_INVALID, "msa_paged_attention_decode: q/out/caches must be 16-byte aligned");
+  DecodeArgs a{};
+  a.q = q; a.ldq = ldq; a.kc = k_cache; a.vc = v_cache; a.num_blocks = num_slots / kBlock;
+  a.heads = heads; a.kv_heads = kv_heads; a.bt = block_tables; a.max_blocks = max_blocks;
+  a.ctx = context_lens; a.qrows = q_rows; a.part_tokens = partition_tokens; a.splits = max_partitions;
+  a.scale_log2 = scale * kLog2e; a.out = out; a.ldo = ldo;
+  if (max_partitions > 1) {
+    const size_t need = msa_paged_attention_decode_workspace_size(num_seqs, heads, head_dim, max_partitions);
+    if (!workspace || workspace_bytes < need)
+      return fail(MSA_ERR_WORKSPACE, "msa_paged_attention_decode: workspace smaller than the workspace size");
+    if (!aligned16(workspace)) return fail(MSA_ERR_INVALID, "msa_paged_attention_decode: workspace must be 16-byte aligned");
+    const size_t slots = (size_t)num_seqs * heads * max_partitions;
+    a.ws_o = (float*)workspace;
+    a.ws_ml = a.ws_o + slots * head_dim;
+  }
+  hipStream_t s = (hipStream_t)stream;
+  switch (heads / kv_heads) {
+    case 1: launch_decode<1>(a, num_seqs, s); break;
+    case 2: launch_decode<2>(a, num_seqs, s); break;
+    case 4: launch_decode<4>(a, num_seqs, s); break;
+    case 8: launch_decode<8>(a, num_seqs, s); break;
+    default: return fail(MSA_ERR_UNSUPPORTED, "msa_paged_attention_decode: heads / kv_heads must be 1, 2, 4 or 8");
+  }
+  int rc = check_launch("msa_paged_attention_decode");
+  if (rc != MSA_OK || max_partitions == 1) return rc;
+  hipLaunchKernelGGL(paged_decode_reduce_kernel, dim3(num_seqs, heads), dim3(kHeadDim), 0, s, a);
+  return check_launch("msa_paged_attention_decode (split merge)");
+}
+
+extern "C" int msa_paged_attention_prefill(const uint16_t* q, int64_t ldq, const uint16_t* k_cache,
+                                           const uint16_t* v_cache, int64_t num_slots, int heads, int kv_heads,
+                                           int head_dim, int block_size, const int32_t* block_tables, int max_blocks,
+                                           const int32_t* seq_info, const int32_t* work, int num_work, float scale,
+                                           uint16_t* out, int64_t ldo, msa_stream_t stream) {
+  using namespace msa;
+  if (num_work == 0) return MSA_OK;
+  if (!q || !k_cache || !v_cache || !block_tables || !seq_info || !work || !out)
+    return fail(MSA_ERR_INVALID, "msa_paged_attention_prefill: null pointer");
+  if (head_dim != kHeadDim) return fail(MSA_ERR_UNSUPPORTED, "msa_paged_attention_prefill: head_dim must be 128");
+  if (block_size != kBlock) return fail(MSA_ERR_UNSUPPORTED, "msa_paged_attention_prefill: block_size must be 16");
+  if (num_work < 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads != 0 || max_blocks <= 0)
+    return fail(MSA_ERR_INVALID, "msa_paged_attention_prefill: bad shape");
+  if (ldq % 8 != 0 || ldo % 4 != 0 || !aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out))
+    return fail(MSA_ERR_INVALID, "msa_paged_attention_prefill: q/out/caches must be 16-byte aligned");
+  PrefillArgs a{};
+  a.q = q; a.ldq = ldq; a.kc = k_cache; a.vc = v_cache; a.num_blocks = num_slots / kBlock;
+  a.heads = heads; a.kv_heads = kv_heads; a.bt = block_tables; a.max_blocks = max_blocks;
+  a.seq_info = seq_info; a.work = work; a.scale_log2 = scale * kLog2e; a.out = out; a.ldo = ldo;
+  const dim3 grid(num_work, kv_heads);
+  hipStream_t s = (hipStream_t)stream;
+  switch (heads / kv_heads) {
+    case 1: hipLaunchKernelGGL(paged_prefill_kernel<1>, grid, dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL(paged_prefill_kernel<2>, grid, dim3(256), 0, s, a); break;
+    case 4: hipLaunchKernelGGL(paged_prefill_kernel<4>, grid, dim3(256), 0, s, a); break;
+    default: return fail(MSA_ERR_UNSUPPORTED, "msa_paged_attention_prefill: heads / kv_heads must be 1, 2 or 4");
+  }
+  return check_launch("msa_paged_attention_prefill");
+}

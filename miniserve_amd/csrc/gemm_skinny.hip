@@ -1,0 +1,352 @@
+// Int8 weight-only linear for decode-shaped batches: y[m, n] = sum_k x[m, k] * bf16(q[n, k] * s[n]).
+//
+// Layout and mapping (gfx950, wave64):
+//  * One workgroup = 4 wavefronts owns a tile of 16*NT weight rows and a range of K; the four waves
+//    split that range in 64-wide chunks (chunk c goes to wave c % 4) and their partial sums meet in
+//    LDS. blockIdx.z walks M in chunks of 64 rows.
+//  * Splitting K across workgroups (blockIdx.y) never synchronizes workgroups: each split writes
+//    its float32 tile with plain stores to partials[split][m][n] and the CONSUMER sums the splits
+//    in a fixed order (bit-reproducible) after the kernel boundary -- a split-K epilogue kernel
+//    here, or the fused residual-add + RMSNorm / q-k-norm + RoPE kernels of the layer. (An
+//    agent-scope fence per workgroup would write back the XCD's L2 each time; on MI355X that cost
+//    dominates these few-microsecond kernels.)
+//  * Per 64-wide K chunk a lane loads 16 contiguous int8 weights of one row (a 16-byte load; the 16
+//    lanes of a row group cover 16 rows, the 4 groups cover the 64 k values) and the matching 16
+//    bf16 activations of each of its M rows (two 16-byte loads per 16-row M tile).
+//  * The weights are dequantized in registers to bf16(q * s) -- q*s is exact in float32 and is
+//    rounded once to bf16, the same value the reference's whole-matrix dequantization
+//    (quant/int8.py:36) produces -- and fed to v_mfma_f32_16x16x32_bf16 with x as the A operand
+//    and the weights as the B operand; accumulation is float32.
+#include "common.h"
+
+namespace msa {
+
+constexpr int kSkinnyWaves = 4;
+constexpr int kSkinnyChunk = 64;
+constexpr int kSkinnyNT = 2;
+constexpr int kEpiPartial = 100;  // internal: write float32 split-K partials
+
+struct SkinnyArgs {
+  const uint16_t* x;
+  int64_t ldx;
+  int m;
+  int k;
+  const int8_t* w;
+  const uint16_t* scale;
+  int n;       // weight rows
+  int n_half;  // MSA_EPI_SILU_MUL: first "up" row
+  uint16_t* y;
+  int64_t ldy;
+  const uint16_t* resid;
+  int64_t ldr;
+  float* partial;  // [k_split][m][n] for kEpiPartial
+  int k_range;     // K handled by one workgroup (multiple of 64)
+};
+
+__device__ __forceinline__ bf16x8 dequant8(uint32_t lo, uint32_t hi, float s) {
+  bf16x8 r;
+  r[0] = (__bf16)((float)(signed char)(lo) * s);
+  r[1] = (__bf16)((float)(signed char)(lo >> 8) * s);
+  r[2] = (__bf16)((float)(signed char)(lo >> 16) * s);
+  r[3] = (__bf16)((float)(signed char)(lo >> 24) * s);
+  r[4] = (__bf16)((float)(signed char)(hi) * s);
+  r[5] = (__bf16)((float)(signed char)(hi >> 8) * s);
+  r[6] = (__bf16)((float)(signed char)(hi >> 16) * s);
+  r[7] = (__bf16)((float)(signed char)(hi >> 24) * s);
+  return r;
+}
+
+__device__ __forceinline__ float silu_mul(float gate_acc, float up_acc) {
+  const float g = round_bf16(gate_acc);
+  const float u = round_bf16(up_acc);
+  return round_bf16(g / (1.0f + expf(-g))) * u;
+}
+
+// Weight row of n-tile nt for lane row j in block nblk.
+template <int NT, int EPI>
+__device__ __forceinline__ int skinny_row(const SkinnyArgs& a, int nblk, int nt, int j) {
+  if constexpr (EPI == MSA_EPI_SILU_MUL) {
+    constexpr int H = NT / 2;
+    return (nt < H ? 0 : a.n_half) + nblk * 16 * H + (nt % H) * 16 + j;
+  } else {
+    return nblk * 16 * NT + nt * 16 + j;
+  }
+}
+
+// Output tile of M tile mt: lane (g, j) holds rows 4g..4g+3, column j of each 16-column n-tile.
+template <int MT, int NT, int EPI>
+__device__ __forceinline__ void skinny_epilogue(const SkinnyArgs& a, int nblk, int mt, const f32x4 (&sum)[NT],
+                                                int lane) {
+  const int j = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int m = blockIdx.z * 64 + mt * 16 + g * 4 + r;
+    if (m >= a.m) continue;
+    if constexpr (EPI == MSA_EPI_SILU_MUL) {
+      constexpr int H = NT / 2;
+#pragma unroll
+      for (int nt = 0; nt < H; ++nt) {
+        const int n = nblk * 16 * H + nt * 16 + j;
+        if (n < a.n_half) a.y[(int64_t)m * a.ldy + n] = f32_to_bf16(silu_mul(sum[nt][r], sum[nt + H][r]));
+      }
+    } else {
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const int n = nblk * 16 * NT + nt * 16 + j;
+        if (n >= a.n) continue;
+        if constexpr (EPI == kEpiPartial) {
+          a.partial[((int64_t)blockIdx.y * a.m + m) * a.n + n] = sum[nt][r];
+        } else {
+          float v = round_bf16(sum[nt][r]);
+          if constexpr (EPI == MSA_EPI_RESIDUAL) v += bf16_to_f32(a.resid[(int64_t)m * a.ldr + n]);
+          a.y[(int64_t)m * a.ldy + n] = f32_to_bf16(v);
+        }
+      }
+    }
+  }
+}
+
+template <int MT, int NT, int EPI>
+__global__ __launch_bounds__(256) void int8_skinny_kernel(SkinnyArgs a) {
+  __shared__ f32x4 red[kSkinnyWaves][MT * NT][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  const int nblk = blockIdx.x, ks = blockIdx.y, mc = blockIdx.z;
+
+  const int8_t* wp[NT];
+  float sc[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    int row = skinny_row<NT, EPI>(a, nblk, nt, j);
+    row = row < a.n ? row : a.n - 1;  // rows past n load row n-1; their outputs are dropped
+    wp[nt] = a.w + (int64_t)row * a.k + g * 16;
+    sc[nt] = bf16_to_f32(a.scale[row]);
+  }
+  const uint16_t* xp[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    int row = mc * 64 + mt * 16 + j;
+    row = row < a.m ? row : a.m - 1;  // rows past m repeat row m-1; their outputs are dropped
+    xp[mt] = a.x + (int64_t)row * a.ldx + g * 16;
+  }
+
+  f32x4 acc[MT][NT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int k_begin = ks * a.k_range;
+  const int k_end = min(a.k, k_begin + a.k_range);
+  for (int kc = k_begin + wave * kSkinnyChunk; kc < k_end; kc += kSkinnyWaves * kSkinnyChunk) {
+    const bool kin = kc + g * 16 < k_end;
+    uint4 wv[NT];
+    uint4 xv[MT][2];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) wv[nt] = kin ? *(const uint4*)(wp[nt] + kc) : uint4{0, 0, 0, 0};
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      xv[mt][0] = kin ? *(const uint4*)(xp[mt] + kc) : uint4{0, 0, 0, 0};
+      xv[mt][1] = kin ? *(const uint4*)(xp[mt] + kc + 8) : uint4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      bf16x8 b[NT];
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+        b[nt] = h == 0 ? dequant8(wv[nt].x, wv[nt].y, sc[nt]) : dequant8(wv[nt].z, wv[nt].w, sc[nt]);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const bf16x8 av = __builtin_bit_cast(bf16x8, xv[mt][h]);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, b[nt], acc[mt][nt], 0, 0, 0);
+      }
+    }
+  }
+
+  // The four waves' partial sums meet in LDS; wave w finishes M tiles w, w+4, ...
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) red[wave][mt * NT + nt][lane] = acc[mt][nt];
+  __syncthreads();
+  for (int mt = wave; mt < MT; mt += kSkinnyWaves) {
+    f32x4 sum[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+      sum[nt] = red[0][mt * NT + nt][lane] + red[1][mt * NT + nt][lane] + red[2][mt * NT + nt][lane] +
+                red[3][mt * NT + nt][lane];
+    skinny_epilogue<MT, NT, EPI>(a, nblk, mt, sum, lane);
+  }
+}
+
+// Sums k_split float32 partials [k_split][m][n] in split order, then applies the epilogue.
+template <int EPI>
+__global__ __launch_bounds__(256) void splitk_epilogue_kernel(const float* __restrict__ part, int k_split, int64_t m,
+                                                              int n, uint16_t* __restrict__ y, int64_t ldy,
+                                                              const uint16_t* resid, int64_t ldr) {
+  const int out_cols = EPI == MSA_EPI_SILU_MUL ? n / 2 : n;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= m * out_cols) return;
+  const int64_t row = idx / out_cols;
+  const int col = (int)(idx % out_cols);
+  const int64_t stride = m * n;
+  float s0 = 0.f, s1 = 0.f;
+  for (int s = 0; s < k_split; ++s) {
+    s0 += part[s * stride + row * n + col];
+    if constexpr (EPI == MSA_EPI_SILU_MUL) s1 += part[s * stride + row * n + col + n / 2];
+  }
+  if constexpr (EPI == MSA_EPI_SILU_MUL) {
+    y[row * ldy + col] = f32_to_bf16(silu_mul(s0, s1));
+  } else {
+    float v = round_bf16(s0);
+    if constexpr (EPI == MSA_EPI_RESIDUAL) v += bf16_to_f32(resid[row * ldr + col]);
+    y[row * ldy + col] = f32_to_bf16(v);
+  }
+}
+
+struct SkinnyPlan {
+  int mt, n_blocks, m_chunks, k_split, k_range;
+};
+
+static SkinnyPlan plan_skinny(int64_t m, int64_t n, int64_t k, int epilogue, int want_split) {
+  SkinnyPlan p{};
+  p.m_chunks = (int)((m + 63) / 64);
+  const int64_t rows_per_m = m < 64 ? m : 64;
+  p.mt = p.m_chunks > 1 ? 4 : (int)((rows_per_m + 15) / 16);
+  const int64_t out_cols = epilogue == MSA_EPI_SILU_MUL ? n / 2 : n;
+  const int per_block = epilogue == MSA_EPI_SILU_MUL ? 16 * kSkinnyNT / 2 : 16 * kSkinnyNT;
+  p.n_blocks = (int)((out_cols + per_block - 1) / per_block);
+  const int64_t chunks = (k + kSkinnyChunk - 1) / kSkinnyChunk;
+  int64_t split = want_split;
+  if (split <= 0) {
+    // Default: split K (which costs a second, summing kernel) only when the output tiles alone
+    // give fewer than 128 workgroups; then aim for about 256, each split a whole multiple of four
+    // 64-wide chunks (one per wave). miniserve_amd.kernels.default_split makes the same choice.
+    const int64_t blocks = (int64_t)p.n_blocks * p.m_chunks;
+    split = blocks >= 128 ? 1 : (256 + blocks - 1) / blocks;
+    const int64_t max_split = chunks / kSkinnyWaves > 0 ? chunks / kSkinnyWaves : 1;
+    split = split > max_split ? max_split : split;
+    const int64_t per = ((chunks + split - 1) / split + 3) / 4 * 4;
+    split = (chunks + per - 1) / per;
+  }
+  split = split < 1 ? 1 : (split > chunks ? chunks : split);
+  p.k_range = (int)(((chunks + split - 1) / split) * kSkinnyChunk);
+  p.k_split = (int)split;  // splits past K write zeros, so the consumer always sums k_split tiles
+  return p;
+}
+
+template <int EPI>
+static void launch_skinny(const SkinnyPlan& p, SkinnyArgs& a, hipStream_t s) {
+  const dim3 grid(p.n_blocks, p.k_split, p.m_chunks);
+  switch (p.mt) {
+    case 1: hipLaunchKernelGGL((int8_skinny_kernel<1, kSkinnyNT, EPI>), grid, dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((int8_skinny_kernel<2, kSkinnyNT, EPI>), grid, dim3(256), 0, s, a); break;
+    case 3: hipLaunchKernelGGL((int8_skinny_kernel<3, kSkinnyNT, EPI>), grid, dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL((int8_skinny_kernel<4, kSkinnyNT, EPI>), grid, dim3(256), 0, s, a); break;
+  }
+}
+
+static int check_linear_args(const char* fn, const uint16_t* x, int64_t m, int64_t k, int64_t ldx,
+                             const int8_t* qweight, const uint16_t* scale, int64_t n) {
+  if (!x || !qweight || !scale) return fail(MSA_ERR_INVALID, std::string(fn) + ": null pointer");
+  if (m < 0 || n <= 0 || k <= 0 || n > 0x7fffffff || k > 0x7fffffff || m > 0x7fffffff)
+    return fail(MSA_ERR_INVALID, std::string(fn) + ": bad shape");
+  if (k % 16 != 0) return fail(MSA_ERR_UNSUPPORTED, std::string(fn) + ": in_features must be a multiple of 16");
+  if (ldx < k || ldx % 8 != 0) return fail(MSA_ERR_INVALID, std::string(fn) + ": ldx must be >= k and a multiple of 8");
+  if (!aligned16(x) || !aligned16(qweight))
+    return fail(MSA_ERR_INVALID, std::string(fn) + ": x and qweight must be 16-byte aligned");
+  return MSA_OK;
+}
+
+}  // namespace msa
+
+extern "C" size_t msa_int8_linear_workspace_size(int64_t m, int64_t n, int64_t k) {
+  if (m <= 0 || n <= 0 || k <= 0) return 0;
+  size_t best = 0;
+  for (int epi = 0; epi < 3; ++epi) {
+    const msa::SkinnyPlan p = msa::plan_skinny(m, n, k, epi, 0);
+    const size_t b = p.k_split > 1 ? (size_t)p.k_split * m * n * sizeof(float) : 0;
+    best = b > best ? b : best;
+  }
+  return best;
+}
+
+extern "C" int msa_int8_linear(const uint16_t* x, int64_t m, int64_t k, int64_t ldx, const int8_t* qweight,
+                               const uint16_t* scale, int64_t n, uint16_t* y, int64_t ldy, int epilogue,
+                               const uint16_t* residual, int64_t ldr, void* workspace, size_t workspace_bytes,
+                               msa_stream_t stream) {
+  using namespace msa;
+  if (m == 0) return MSA_OK;
+  int rc = check_linear_args("msa_int8_linear", x, m, k, ldx, qweight, scale, n);
+  if (rc != MSA_OK) return rc;
+  if (!y) return fail(MSA_ERR_INVALID, "msa_int8_linear: null pointer");
+  if (epilogue < 0 || epilogue > 2) return fail(MSA_ERR_INVALID, "msa_int8_linear: unknown epilogue");
+  if (epilogue == MSA_EPI_SILU_MUL && n % 2 != 0) return fail(MSA_ERR_INVALID, "msa_int8_linear: SILU_MUL needs an even n");
+  const int64_t out_cols = epilogue == MSA_EPI_SILU_MUL ? n / 2 : n;
+  if (ldy < out_cols) return fail(MSA_ERR_INVALID, "msa_int8_linear: ldy too small");
+  if (epilogue == MSA_EPI_RESIDUAL && (!residual || ldr < n))
+    return fail(MSA_ERR_INVALID, "msa_int8_linear: residual epilogue needs residual with ldr >= n");
+
+  SkinnyPlan p = plan_skinny(m, n, k, epilogue, 0);
+  const size_t need = p.k_split > 1 ? (size_t)p.k_split * m * n * sizeof(float) : 0;
+  if (p.k_split > 1 && (!workspace || workspace_bytes < need)) p = plan_skinny(m, n, k, epilogue, 1);
+  SkinnyArgs a{};
+  a.x = x; a.ldx = ldx; a.m = (int)m; a.k = (int)k;
+  a.w = qweight; a.scale = scale; a.n = (int)n; a.n_half = (int)(n / 2);
+  a.y = y; a.ldy = ldy; a.resid = residual; a.ldr = ldr;
+  a.k_range = p.k_range;
+  hipStream_t s = (hipStream_t)stream;
+  if (p.k_split > 1) {
+    // Partials are computed without the SILU row pairing, so plan the partial pass as a plain GEMM.
+    SkinnyPlan pp = plan_skinny(m, n, k, MSA_EPI_NONE, p.k_split);
+    a.k_range = pp.k_range;
+    a.partial = (float*)workspace;
+    launch_skinny<kEpiPartial>(pp, a, s);
+    rc = check_launch("msa_int8_linear (split-K pass)");
+    if (rc != MSA_OK) return rc;
+    const int64_t total = m * out_cols;
+    const unsigned blocks = (unsigned)((total + 255) / 256);
+    switch (epilogue) {
+      case MSA_EPI_NONE:
+        hipLaunchKernelGGL(splitk_epilogue_kernel<MSA_EPI_NONE>, dim3(blocks), dim3(256), 0, s, a.partial, pp.k_split,
+                           m, (int)n, y, ldy, residual, ldr);
+        break;
+      case MSA_EPI_SILU_MUL:
+        hipLaunchKernelGGL(splitk_epilogue_kernel<MSA_EPI_SILU_MUL>, dim3(blocks), dim3(256), 0, s, a.partial,
+                           pp.k_split, m, (int)n, y, ldy, residual, ldr);
+        break;
+      default:
+        hipLaunchKernelGGL(splitk_epilogue_kernel<MSA_EPI_RESIDUAL>, dim3(blocks), dim3(256), 0, s, a.partial,
+                           pp.k_split, m, (int)n, y, ldy, residual, ldr);
+        break;
+    }
+    return check_launch("msa_int8_linear (split-K epilogue)");
+  }
+  switch (epilogue) {
+    case MSA_EPI_NONE: launch_skinny<MSA_EPI_NONE>(p, a, s); break;
+    case MSA_EPI_SILU_MUL: launch_skinny<MSA_EPI_SILU_MUL>(p, a, s); break;
+    default: launch_skinny<MSA_EPI_RESIDUAL>(p, a, s); break;
+  }
+  return check_launch("msa_int8_linear");
+}
+
+extern "C" int msa_int8_linear_splitk(const uint16_t* x, int64_t m, int64_t k, int64_t ldx, const int8_t* qweight,
+                                      const uint16_t* scale, int64_t n, int k_split, float* partials,
+                                      msa_stream_t stream) {
+  using namespace msa;
+  if (m == 0) return MSA_OK;
+  int rc = check_linear_args("msa_int8_linear_splitk", x, m, k, ldx, qweight, scale, n);
+  if (rc != MSA_OK) return rc;
+  if (!partials) return fail(MSA_ERR_INVALID, "msa_int8_linear_splitk: null partials");
+  if (k_split < 1 || (int64_t)k_split > (k + kSkinnyChunk - 1) / kSkinnyChunk)
+    return fail(MSA_ERR_INVALID, "msa_int8_linear_splitk: k_split must be in [1, ceil(k / 64)]");
+  SkinnyPlan p = plan_skinny(m, n, k, MSA_EPI_NONE, k_split);
+  SkinnyArgs a{};
+  a.x = x; a.ldx = ldx; a.m = (int)m; a.k = (int)k;
+  a.w = qweight; a.scale = scale; a.n = (int)n; a.n_half = (int)(n / 2);
+  a.partial = partials; a.k_range = p.k_range;
+  launch_skinny<kEpiPartial>(p, a, (hipStream_t)stream);
+  return check_launch("msa_int8_linear_splitk");
+}

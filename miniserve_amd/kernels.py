@@ -1,0 +1,346 @@
+"""Tensor-level wrappers over the C ABI: argument checks, output allocation, workspaces, streams.
+
+Every op launches on the current HIP stream of its tensors' device and never synchronizes. Bad
+arguments raise ``RuntimeError`` before anything is launched (the convention of a TORCH_CHECK).
+Workspaces are device scratch buffers owned here (one per kind and device, grown on demand and
+reserved before any graph capture); kernels never need them zeroed.
+"""
+
+from __future__ import annotations
+
+from ctypes import c_void_p
+
+import torch
+from torch import Tensor
+
+from miniserve_amd import _native
+
+EPI_NONE, EPI_SILU_MUL, EPI_RESIDUAL = 0, 1, 2
+
+
+def _check(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _ptr(t: Tensor | None) -> c_void_p:
+    return c_void_p(t.data_ptr() if t is not None else 0)
+
+
+def _stream(t: Tensor) -> c_void_p:
+    return c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _on_gpu(*ts: Tensor) -> None:
+    dev = ts[0].device
+    for t in ts:
+        _check(t.is_cuda, "miniserve_amd ops run on the GPU only (got a CPU tensor)")
+        _check(t.device == dev, "all tensors of an op must be on one device")
+
+
+class _Workspaces:
+    def __init__(self) -> None:
+        self._bufs: dict[tuple[str, int], Tensor] = {}
+
+    def get(self, kind: str, device: torch.device, nbytes: int) -> Tensor | None:
+        if nbytes == 0:
+            return None
+        key = (kind, device.index or 0)
+        buf = self._bufs.get(key)
+        if buf is None or buf.numel() < nbytes:
+            _check(
+                not torch.cuda.is_current_stream_capturing(),
+                f"workspace '{kind}' must be reserved before graph capture (need {nbytes} bytes)",
+            )
+            size = max(nbytes, 2 * (buf.numel() if buf is not None else 0), 1 << 20)
+            buf = torch.empty(size, dtype=torch.uint8, device=device)
+            self._bufs[key] = buf
+        return buf
+
+    def reserve(self, kind: str, device: torch.device, nbytes: int) -> None:
+        self.get(kind, device, nbytes)
+
+
+workspaces = _Workspaces()
+
+
+# ---- int8 linears ---------------------------------------------------------------------------------
+
+
+def int8_quantize(weight: Tensor) -> tuple[Tensor, Tensor]:
+    """(qweight int8 [out, in], scale bf16 [out]) -- quant/int8.py:25-33 on the GPU."""
+    _on_gpu(weight)
+    _check(weight.dim() == 2, "int8_quantize expects a 2-D weight")
+    _check(weight.dtype in (torch.bfloat16, torch.float32), "int8_quantize supports bf16 or float32 weights")
+    w = weight.detach().contiguous()
+    rows, cols = w.shape
+    q = torch.empty(rows, cols, dtype=torch.int8, device=w.device)
+    s = torch.empty(rows, dtype=torch.bfloat16, device=w.device)
+    dtype_code = 0 if w.dtype == torch.bfloat16 else 1
+    _native.call("msa_int8_quantize", _ptr(w), dtype_code, rows, cols, _ptr(q), _ptr(s), _stream(w))
+    return q, s
+
+
+def int8_linear(
+    x: Tensor,
+    qweight: Tensor,
+    scale: Tensor,
+    epilogue: int = EPI_NONE,
+    residual: Tensor | None = None,
+    out: Tensor | None = None,
+) -> Tensor:
+    """y = x @ bf16(qweight * scale)^T (quant/int8.py:35-37) with an optional fused epilogue.
+
+    x [..., in] bf16. EPI_SILU_MUL treats the rows as [gate | up] and returns silu(g) * u
+    [..., out/2]; EPI_RESIDUAL returns residual + y.
+    """
+    _on_gpu(x, qweight, scale)
+    _check(x.dtype == torch.bfloat16, "int8_linear: activations must be bf16")
+    _check(qweight.dtype == torch.int8 and qweight.dim() == 2 and qweight.is_contiguous(), "int8_linear: bad qweight")
+    _check(scale.dtype == torch.bfloat16 and scale.numel() == qweight.shape[0], "int8_linear: bad scale")
+    n, k = qweight.shape
+    _check(x.shape[-1] == k, f"int8_linear: x has {x.shape[-1]} features, weight expects {k}")
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, k)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 != 0 or x2.data_ptr() % 16 != 0:
+        x2 = x2.contiguous()
+    m = x2.shape[0]
+    cols = n // 2 if epilogue == EPI_SILU_MUL else n
+    if out is None:
+        out = torch.empty(*lead, cols, dtype=torch.bfloat16, device=x.device)
+    _check(out.shape[-1] == cols and out.is_contiguous(), "int8_linear: bad out")
+    r2 = None
+    if epilogue == EPI_RESIDUAL:
+        _check(residual is not None and residual.shape[-1] == n, "int8_linear: residual epilogue needs residual")
+        r2 = residual.reshape(-1, n)
+        _check(r2.stride(-1) == 1 and r2.dtype == torch.bfloat16, "int8_linear: residual must be row-major bf16")
+    ws_bytes = _native.query("msa_int8_linear_workspace_size", m, n, k) if m else 0
+    ws = workspaces.get("linear", x.device, ws_bytes)
+    _native.call(
+        "msa_int8_linear", _ptr(x2), m, k, x2.stride(0), _ptr(qweight), _ptr(scale), n, _ptr(out), cols, epilogue,
+        _ptr(r2), r2.stride(0) if r2 is not None else 0, _ptr(ws), ws.numel() if ws is not None else 0, _stream(x),
+    )
+    return out
+
+
+def default_split(m: int, n: int, k: int) -> int:
+    """K splits for a split-K linear: none when the 32-row x 64-row output tiles give 128+
+    workgroups, else about 256 workgroups, each split a whole multiple of four 64-wide K chunks
+    (one per wavefront). The C ABI's default plan for msa_int8_linear makes the same choice."""
+    chunks = -(-k // 64)
+    blocks = -(-n // 32) * -(-m // 64)
+    if blocks >= 128:
+        return 1
+    split = max(1, min(-(-256 // blocks), max(1, chunks // 4)))
+    per = -(-chunks // split)
+    per = -(-per // 4) * 4
+    return max(1, -(-chunks // per))
+
+
+def int8_linear_splitk(x: Tensor, qweight: Tensor, scale: Tensor, k_split: int) -> Tensor:
+    """float32 partials [k_split, m, n] of x @ bf16(qweight * scale)^T over k_split ranges of K;
+    bf16(partials.sum(0)) is the linear's output. Consumers sum them inside their own kernel."""
+    _on_gpu(x, qweight, scale)
+    _check(x.dtype == torch.bfloat16 and x.dim() == 2 and x.stride(-1) == 1, "int8_linear_splitk: x [m, k] bf16")
+    _check(qweight.dtype == torch.int8 and qweight.is_contiguous(), "int8_linear_splitk: bad qweight")
+    n, k = qweight.shape
+    m = x.shape[0]
+    part = torch.empty(k_split, m, n, dtype=torch.float32, device=x.device)
+    _native.call("msa_int8_linear_splitk", _ptr(x), m, k, x.stride(0), _ptr(qweight), _ptr(scale), n, k_split,
+                 _ptr(part), _stream(x))
+    return part
+
+
+def splitk_add_rmsnorm(
+    partials: Tensor, residual: Tensor, weight: Tensor, eps: float, residual_out: Tensor | None = None
+) -> tuple[Tensor, Tensor]:
+    """(bf16(residual + bf16(sum of partials)), RMSNorm of it) in one kernel."""
+    _on_gpu(partials, residual, weight)
+    k_split, rows, dim = partials.shape
+    _check(partials.dtype == torch.float32 and partials.is_contiguous(), "splitk_add_rmsnorm: partials")
+    _check(residual.shape == (rows, dim) and residual.is_contiguous(), "splitk_add_rmsnorm: residual")
+    if residual_out is None:
+        residual_out = torch.empty_like(residual)
+    out = torch.empty_like(residual)
+    _native.call("msa_splitk_add_rmsnorm", _ptr(partials), k_split, _ptr(residual), _ptr(residual_out),
+                 _ptr(weight), _ptr(out), rows, dim, float(eps), _stream(partials))
+    return residual_out, out
+
+
+def qk_norm_rope_cache_splitk(
+    partials: Tensor,
+    heads: int,
+    kv_heads: int,
+    head_dim: int,
+    q_norm_w: Tensor,
+    k_norm_w: Tensor,
+    eps: float,
+    cos: Tensor,
+    sin: Tensor,
+    slot_mapping: Tensor,
+    k_cache: Tensor,
+    v_cache: Tensor,
+) -> Tensor:
+    """qk_norm_rope_cache whose qkv rows arrive as split-K partials [k_split, T, (H+2KVH)*D]."""
+    _on_gpu(partials, q_norm_w, k_norm_w, cos, sin, slot_mapping, k_cache, v_cache)
+    k_split, t, cols = partials.shape
+    _check(cols == (heads + 2 * kv_heads) * head_dim and partials.is_contiguous(), "qkv partials shape")
+    _check(cos.shape == (t, head_dim) and sin.shape == (t, head_dim) and cos.dtype == torch.float32, "cos/sin")
+    _check(slot_mapping.dtype == torch.int64 and slot_mapping.numel() == t, "slot_mapping")
+    _check(k_cache.shape[-2:] == (kv_heads, head_dim) and k_cache.is_contiguous() and v_cache.is_contiguous(), "caches")
+    q = torch.empty(t, heads, head_dim, dtype=torch.bfloat16, device=partials.device)
+    _native.call(
+        "msa_qk_norm_rope_cache_splitk", _ptr(partials), k_split, t, heads, kv_heads, head_dim, _ptr(q_norm_w),
+        _ptr(k_norm_w), float(eps), _ptr(cos), _ptr(sin), _ptr(slot_mapping), _ptr(q), _ptr(k_cache), _ptr(v_cache),
+        k_cache.shape[0], _stream(partials),
+    )
+    return q
+
+
+# ---- norms / RoPE / cache -------------------------------------------------------------------------
+
+
+def rmsnorm(x: Tensor, weight: Tensor, eps: float, out: Tensor | None = None) -> Tensor:
+    """RMSNorm over the last dim (model/layers.py:18-22)."""
+    _on_gpu(x, weight)
+    _check(x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16, "rmsnorm: bf16 only")
+    dim = x.shape[-1]
+    _check(weight.numel() == dim, "rmsnorm: weight size mismatch")
+    x2 = x.reshape(-1, dim)
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    if out is None:
+        out = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
+    o2 = out.view(-1, dim)
+    _native.call("msa_rmsnorm", _ptr(x2), x2.stride(0), _ptr(weight), _ptr(o2), o2.stride(0), x2.shape[0], dim,
+                 float(eps), _stream(x))
+    return out
+
+
+def add_rmsnorm(
+    residual: Tensor, delta: Tensor, weight: Tensor, eps: float, residual_out: Tensor | None = None
+) -> tuple[Tensor, Tensor]:
+    """(bf16(residual + delta), RMSNorm of it) -- model/qwen3.py:121-122 fused."""
+    _on_gpu(residual, delta, weight)
+    _check(residual.shape == delta.shape and residual.is_contiguous() and delta.is_contiguous(), "add_rmsnorm: shapes")
+    dim = residual.shape[-1]
+    if residual_out is None:
+        residual_out = torch.empty_like(residual)
+    out = torch.empty_like(residual)
+    _native.call("msa_add_rmsnorm", _ptr(residual), _ptr(delta), _ptr(residual_out), _ptr(weight), _ptr(out),
+                 residual.numel() // dim, dim, float(eps), _stream(residual))
+    return residual_out, out
+
+
+def qk_norm_rope_cache(
+    qkv: Tensor,
+    heads: int,
+    kv_heads: int,
+    head_dim: int,
+    q_norm_w: Tensor,
+    k_norm_w: Tensor,
+    eps: float,
+    cos: Tensor,
+    sin: Tensor,
+    slot_mapping: Tensor,
+    k_cache: Tensor,
+    v_cache: Tensor,
+) -> Tensor:
+    """q/k-norm + RoPE of the fused qkv rows, k/v written to the cache; returns q [T, H, D]."""
+    _on_gpu(qkv, q_norm_w, k_norm_w, cos, sin, slot_mapping, k_cache, v_cache)
+    t = qkv.shape[0]
+    _check(qkv.shape[-1] == (heads + 2 * kv_heads) * head_dim and qkv.stride(-1) == 1, "qk_norm_rope_cache: qkv shape")
+    _check(cos.dtype == torch.float32 and cos.shape == (t, head_dim) and cos.is_contiguous(), "qk_norm_rope_cache: cos")
+    _check(sin.dtype == torch.float32 and sin.shape == (t, head_dim) and sin.is_contiguous(), "qk_norm_rope_cache: sin")
+    _check(slot_mapping.dtype == torch.int64 and slot_mapping.numel() == t, "qk_norm_rope_cache: slot_mapping")
+    _check(k_cache.is_contiguous() and v_cache.is_contiguous() and k_cache.shape == v_cache.shape, "caches")
+    _check(k_cache.shape[-2:] == (kv_heads, head_dim), "qk_norm_rope_cache: cache layout [slots, KVH, D]")
+    q = torch.empty(t, heads, head_dim, dtype=torch.bfloat16, device=qkv.device)
+    _native.call(
+        "msa_qk_norm_rope_cache", _ptr(qkv), qkv.stride(0), t, heads, kv_heads, head_dim, _ptr(q_norm_w),
+        _ptr(k_norm_w), float(eps), _ptr(cos), _ptr(sin), _ptr(slot_mapping), _ptr(q), _ptr(k_cache),
+        _ptr(v_cache), k_cache.shape[0], _stream(qkv),
+    )
+    return q
+
+
+def reshape_and_cache(k: Tensor, v: Tensor, k_cache: Tensor, v_cache: Tensor, slot_mapping: Tensor) -> None:
+    """k_cache[slot_mapping] = k; v_cache[slot_mapping] = v (attention/backends.py:159-160)."""
+    _on_gpu(k, v, k_cache, v_cache, slot_mapping)
+    t, kvh, d = k.shape
+    _check(v.shape == k.shape and k_cache.shape[-2:] == (kvh, d), "reshape_and_cache: shapes")
+    _check(slot_mapping.dtype == torch.int64 and slot_mapping.numel() == t, "reshape_and_cache: slot_mapping")
+    k2 = k if k.stride(-1) == 1 and k.stride(-2) == d else k.contiguous()
+    v2 = v if v.stride(-1) == 1 and v.stride(-2) == d else v.contiguous()
+    _native.call("msa_reshape_and_cache", _ptr(k2), k2.stride(0), _ptr(v2), v2.stride(0), t, kvh, d,
+                 _ptr(slot_mapping), _ptr(k_cache), _ptr(v_cache), k_cache.shape[0], _stream(k))
+
+
+# ---- paged attention ------------------------------------------------------------------------------
+
+
+def decode_splits(num_seqs: int, kv_heads: int, max_blocks: int) -> tuple[int, int]:
+    """(partition_tokens, partitions) for the decode kernel: one workgroup of eight wavefronts per
+    (sequence, KV head) when that gives 256+ workgroups; otherwise split each sequence's keys
+    across workgroups (at least eight 16-token blocks, one per wavefront, in each)."""
+    wgs = max(1, num_seqs * kv_heads)
+    splits = 1 if wgs >= 256 else min(-(-512 // wgs), max(1, max_blocks // 8))
+    per_blocks = -(-max_blocks // splits)
+    return per_blocks * 16, -(-max_blocks // per_blocks)
+
+
+def paged_attention_decode(
+    q: Tensor,
+    k_cache: Tensor,
+    v_cache: Tensor,
+    block_tables: Tensor,
+    context_lens: Tensor,
+    q_rows: Tensor,
+    partition_tokens: int,
+    max_partitions: int,
+    scale: float,
+    out: Tensor,
+    block_size: int = 16,
+) -> Tensor:
+    """Decode attention through the block table; (partition_tokens, max_partitions) as from
+    ``decode_splits``; partition_tokens * max_partitions must cover the block-table width."""
+    _on_gpu(q, k_cache, v_cache, block_tables, context_lens, q_rows, out)
+    _, heads, d = q.shape
+    kvh = k_cache.shape[1]
+    num = context_lens.numel()
+    _check(block_tables.dtype == torch.int32 and block_tables.is_contiguous() and block_tables.shape[0] == num,
+           "paged_attention_decode: block_tables")
+    _check(context_lens.dtype == torch.int32 and q_rows.dtype == torch.int32, "paged_attention_decode: int32 metadata")
+    ws_bytes = _native.query("msa_paged_attention_decode_workspace_size", num, heads, d, max_partitions)
+    ws = workspaces.get("attention", q.device, ws_bytes)
+    _native.call(
+        "msa_paged_attention_decode", _ptr(q), q.stride(0), _ptr(k_cache), _ptr(v_cache), k_cache.shape[0], heads,
+        kvh, d, block_size, _ptr(block_tables), block_tables.shape[1], _ptr(context_lens), _ptr(q_rows), num,
+        partition_tokens, max_partitions, float(scale), _ptr(out), out.stride(0), _ptr(ws),
+        ws.numel() if ws is not None else 0, _stream(q),
+    )
+    return out
+
+
+def paged_attention_prefill(
+    q: Tensor,
+    k_cache: Tensor,
+    v_cache: Tensor,
+    block_tables: Tensor,
+    seq_info: Tensor,
+    work: Tensor,
+    scale: float,
+    out: Tensor,
+    block_size: int = 16,
+) -> Tensor:
+    _on_gpu(q, k_cache, v_cache, block_tables, seq_info, work, out)
+    _, heads, d = q.shape
+    kvh = k_cache.shape[1]
+    _check(seq_info.dtype == torch.int32 and work.dtype == torch.int32 and block_tables.dtype == torch.int32,
+           "paged_attention_prefill: int32 metadata")
+    _native.call(
+        "msa_paged_attention_prefill", _ptr(q), q.stride(0), _ptr(k_cache), _ptr(v_cache), k_cache.shape[0], heads,
+        kvh, d, block_size, _ptr(block_tables), block_tables.shape[1], _ptr(seq_info), _ptr(work), work.shape[0],
+        float(scale), _ptr(out), out.stride(0), _stream(q),
+    )
+    return out

@@ -1,0 +1,201 @@
+"""Qwen3 (dense) over a flat continuous batch, on the HIP kernels (reference:
+src/miniserve/model/qwen3.py).
+
+Same module tree, parameter names and call signatures as the reference, so checkpoints, the
+loader's fused row order ([q | k | v] and [gate | up]) and the runner plug in unchanged, and each
+module's ``forward`` computes what the reference's does.
+
+Once every linear is int8, ``Qwen3ForCausalLM.forward`` runs the layers as one fused pipeline
+that crosses module boundaries (8 launches per layer, no workgroup ever waits on another):
+  int8 qkv (split-K partials) -> [sum + q/k-norm + RoPE + KV write] -> paged attention
+  -> int8 o (partials) -> [sum + residual add + post-attention RMSNorm]
+  -> int8 gate_up with silu*up epilogue -> int8 down (partials)
+  -> [sum + residual add + the NEXT layer's input RMSNorm (the final norm after the last layer)]
+Bracketed steps are single kernels. Logits are computed separately, only for sampled rows.
+"""
+
+from __future__ import annotations
+
+import json
+from dataclasses import dataclass
+from pathlib import Path
+from typing import Any
+
+import torch.nn.functional as F
+from torch import Tensor, nn
+
+from miniserve_amd import kernels
+from miniserve_amd.attention.backends import AttentionMetadata, attend
+from miniserve_amd.model.layers import RMSNorm, RotaryEmbedding, SwiGLU
+from miniserve_amd.quant.int8 import Int8Linear
+
+
+@dataclass(frozen=True)
+class Qwen3Config:
+    """model/qwen3.py:18-62."""
+
+    vocab_size: int
+    hidden_size: int
+    intermediate_size: int
+    num_hidden_layers: int
+    num_attention_heads: int
+    num_key_value_heads: int
+    head_dim: int
+    rms_norm_eps: float
+    rope_theta: float
+    max_position_embeddings: int
+    tie_word_embeddings: bool
+
+    @classmethod
+    def from_dict(cls, d: dict[str, Any]) -> Qwen3Config:
+        rope = d.get("rope_parameters") or {}
+        return cls(
+            vocab_size=d["vocab_size"],
+            hidden_size=d["hidden_size"],
+            intermediate_size=d["intermediate_size"],
+            num_hidden_layers=d["num_hidden_layers"],
+            num_attention_heads=d["num_attention_heads"],
+            num_key_value_heads=d["num_key_value_heads"],
+            head_dim=d.get("head_dim") or d["hidden_size"] // d["num_attention_heads"],
+            rms_norm_eps=d["rms_norm_eps"],
+            rope_theta=float(d.get("rope_theta") or rope.get("rope_theta") or 10000.0),
+            max_position_embeddings=d["max_position_embeddings"],
+            tie_word_embeddings=bool(d.get("tie_word_embeddings", False)),
+        )
+
+    @classmethod
+    def from_pretrained(cls, model_dir: str | Path) -> Qwen3Config:
+        return cls.from_dict(json.loads((Path(model_dir) / "config.json").read_text()))
+
+    def kv_bytes_per_token(self, dtype_bytes: int) -> int:
+        """K and V for every layer: 2 x layers x kv_heads x head_dim x bytes."""
+        return 2 * self.num_hidden_layers * self.num_key_value_heads * self.head_dim * dtype_bytes
+
+
+class Qwen3Attention(nn.Module):
+    def __init__(self, cfg: Qwen3Config) -> None:
+        super().__init__()
+        self.num_heads = cfg.num_attention_heads
+        self.num_kv_heads = cfg.num_key_value_heads
+        self.head_dim = cfg.head_dim
+        self.q_size = self.num_heads * self.head_dim
+        self.kv_size = self.num_kv_heads * self.head_dim
+        self.scale = self.head_dim**-0.5
+        self.qkv_proj: nn.Module = nn.Linear(cfg.hidden_size, self.q_size + 2 * self.kv_size, bias=False)
+        self.o_proj: nn.Module = nn.Linear(self.q_size, cfg.hidden_size, bias=False)
+        self.q_norm = RMSNorm(self.head_dim, cfg.rms_norm_eps)
+        self.k_norm = RMSNorm(self.head_dim, cfg.rms_norm_eps)
+
+    def forward(
+        self,
+        x: Tensor,
+        cos: Tensor,
+        sin: Tensor,
+        k_cache: Tensor,
+        v_cache: Tensor,
+        meta: AttentionMetadata,
+    ) -> Tensor:
+        """model/qwen3.py:84-101: qkv -> q/k-norm -> RoPE -> paged attention -> o."""
+        t = x.shape[0]
+        qkv = self.qkv_proj(x)
+        q = kernels.qk_norm_rope_cache(
+            qkv, self.num_heads, self.num_kv_heads, self.head_dim, self.q_norm.weight, self.k_norm.weight,
+            self.q_norm.eps, cos, sin, meta.slot_mapping, k_cache, v_cache,
+        )
+        out = attend(q, k_cache, v_cache, meta, self.scale)
+        result: Tensor = self.o_proj(out.view(t, self.q_size))
+        return result
+
+
+class Qwen3DecoderLayer(nn.Module):
+    def __init__(self, cfg: Qwen3Config) -> None:
+        super().__init__()
+        self.input_layernorm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps)
+        self.self_attn = Qwen3Attention(cfg)
+        self.post_attention_layernorm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps)
+        self.mlp = SwiGLU(cfg.hidden_size, cfg.intermediate_size)
+
+    def forward(
+        self,
+        x: Tensor,
+        cos: Tensor,
+        sin: Tensor,
+        k_cache: Tensor,
+        v_cache: Tensor,
+        meta: AttentionMetadata,
+    ) -> Tensor:
+        """x += attn(norm(x)); x += mlp(norm(x))  (model/qwen3.py:112-122)."""
+        a = self.self_attn(self.input_layernorm(x), cos, sin, k_cache, v_cache, meta)
+        x2, h = kernels.add_rmsnorm(x, a, self.post_attention_layernorm.weight, self.post_attention_layernorm.eps)
+        return self.mlp(h, residual=x2)
+
+
+class Qwen3ForCausalLM(nn.Module):
+    def __init__(self, cfg: Qwen3Config, max_positions: int) -> None:
+        super().__init__()
+        self.cfg = cfg
+        self.embed_tokens = nn.Embedding(cfg.vocab_size, cfg.hidden_size)
+        self.layers = nn.ModuleList(Qwen3DecoderLayer(cfg) for _ in range(cfg.num_hidden_layers))
+        self.norm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps)
+        self.rotary = RotaryEmbedding(cfg.head_dim, max_positions, cfg.rope_theta)
+        self.lm_head: nn.Linear | None = (
+            None if cfg.tie_word_embeddings else nn.Linear(cfg.hidden_size, cfg.vocab_size, bias=False)
+        )
+
+    def forward(
+        self,
+        input_ids: Tensor,
+        positions: Tensor,
+        kv_caches: list[tuple[Tensor, Tensor]],
+        meta: AttentionMetadata,
+    ) -> Tensor:
+        """input_ids, positions: [T]. Returns final hidden states [T, hidden] (qwen3.py:140-153)."""
+        x = self.embed_tokens(input_ids)
+        cos, sin = self.rotary(positions)
+        if len(kv_caches) != len(self.layers):
+            raise ValueError(f"{len(kv_caches)} KV caches for {len(self.layers)} layers")
+        if self._all_int8():
+            return self._fused_forward(x, cos, sin, kv_caches, meta)
+        for layer, (k_cache, v_cache) in zip(self.layers, kv_caches, strict=True):
+            x = layer(x, cos, sin, k_cache, v_cache, meta)
+        out: Tensor = self.norm(x)
+        return out
+
+    def _all_int8(self) -> bool:
+        return all(
+            isinstance(m, Int8Linear)
+            for layer in self.layers
+            for m in (layer.self_attn.qkv_proj, layer.self_attn.o_proj, layer.mlp.gate_up_proj, layer.mlp.down_proj)
+        )
+
+    def _fused_forward(
+        self, x: Tensor, cos: Tensor, sin: Tensor, kv_caches: list[tuple[Tensor, Tensor]], meta: AttentionMetadata
+    ) -> Tensor:
+        """The layer loop with every residual add / RMSNorm / split-K reduction fused into the
+        kernel that consumes it; returns norm(x_L), the same value as the module-by-module loop."""
+        cfg = self.cfg
+        eps = cfg.rms_norm_eps
+        t = x.shape[0]
+        layers = self.layers
+        h = kernels.rmsnorm(x, layers[0].input_layernorm.weight, eps)
+        for i, (layer, (k_cache, v_cache)) in enumerate(zip(layers, kv_caches, strict=True)):
+            attn, mlp = layer.self_attn, layer.mlp
+            qkv, o, gu, dn = attn.qkv_proj, attn.o_proj, mlp.gate_up_proj, mlp.down_proj
+            part = kernels.int8_linear_splitk(h, qkv.qweight, qkv.scale, kernels.default_split(t, qkv.out_features, qkv.in_features))
+            q = kernels.qk_norm_rope_cache_splitk(
+                part, attn.num_heads, attn.num_kv_heads, attn.head_dim, attn.q_norm.weight, attn.k_norm.weight,
+                attn.q_norm.eps, cos, sin, meta.slot_mapping, k_cache, v_cache,
+            )
+            a = attend(q, k_cache, v_cache, meta, attn.scale).view(t, attn.q_size)
+            part = kernels.int8_linear_splitk(a, o.qweight, o.scale, kernels.default_split(t, o.out_features, o.in_features))
+            x, h = kernels.splitk_add_rmsnorm(part, x, layer.post_attention_layernorm.weight, eps)
+            act = gu(h, epilogue=kernels.EPI_SILU_MUL)
+            part = kernels.int8_linear_splitk(act, dn.qweight, dn.scale, kernels.default_split(t, dn.out_features, dn.in_features))
+            nxt = layers[i + 1].input_layernorm.weight if i + 1 < len(layers) else self.norm.weight
+            x, h = kernels.splitk_add_rmsnorm(part, x, nxt, eps)
+        return h
+
+    def compute_logits(self, hidden: Tensor) -> Tensor:
+        """[n, hidden] -> [n, vocab] float32, the product in bf16 (qwen3.py:155-158)."""
+        weight = self.embed_tokens.weight if self.lm_head is None else self.lm_head.weight
+        return F.linear(hidden, weight).float()

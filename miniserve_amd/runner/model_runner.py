@@ -1,0 +1,195 @@
+"""Turn scheduled sequences into one forward pass and greedy next tokens (reference:
+src/miniserve/runner/model_runner.py).
+
+The runner owns the KV pool ``[layers, 2, num_blocks * block_size, kv_heads, head_dim]``
+(model_runner.py:77-94, zero-filled so masked slots never hold NaN), flattens every scheduled
+sequence's new tokens into one batch with per-token positions and slots (model_runner.py:162-205),
+computes logits only for rows that are sampled and syncs once per step (model_runner.py:207-239).
+The engine, scheduler and block manager stay with the caller: a ``ScheduledChunk`` carries what the
+runner reads from the reference's ``ScheduledSeq`` (token ids, tokens already computed, tokens
+scheduled now, block table).
+
+Pure decode steps (every sequence schedules one token) run as a captured HIP graph per batch size
+(``use_graphs``): the forward, the LM head and the greedy argmax replay with one launch; the
+step's ids, positions, slots, context lengths and block tables are copied into the graph's
+static device buffers from one pinned host buffer first. This is the reference's own next step
+(its README's "CUDA graphs" item): its decode step is launch-bound.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+from torch import Tensor
+
+from miniserve_amd.attention.backends import AttentionMetadata, DecodePlan, SeqChunk, build_attention_metadata
+from miniserve_amd.model.qwen3 import Qwen3ForCausalLM
+from miniserve_amd.runner.sampler import sample
+from miniserve_amd.utils import to_device
+
+
+@dataclass
+class ScheduledChunk:
+    token_ids: list[int]
+    num_computed: int
+    num_new: int
+    block_table: list[int]
+
+
+@dataclass
+class StepInputs:
+    input_ids: Tensor
+    positions: Tensor
+    attn: AttentionMetadata
+    logits_rows: Tensor
+    sample_idx: list[int]
+
+
+class CapturedDecode:
+    """One decode step of ``batch`` sequences captured as a HIP graph with static inputs.
+
+    Block tables are ``max_blocks`` wide (the longest context the graph accepts is
+    ``max_blocks * block_size`` tokens); the attention launch shape depends only on that width.
+    """
+
+    def __init__(self, runner: ModelRunner, batch: int, max_blocks: int) -> None:
+        dev = runner.device
+        self.batch, self.max_blocks = batch, max_blocks
+        self.host = torch.zeros(3 * batch + 2 * batch + batch * max_blocks, dtype=torch.int64, pin_memory=True)
+        self.dev = torch.zeros_like(self.host, device=dev)
+        b = batch
+        self.ids, self.pos, self.slots = self.dev[:b], self.dev[b : 2 * b], self.dev[2 * b : 3 * b]
+        meta32 = self.dev[3 * b :].view(torch.int32)  # q_rows | context_lens | tables, as int32
+        plan = DecodePlan(meta32[:b], meta32[b : 2 * b], meta32[2 * b : 2 * b + b * max_blocks].view(b, max_blocks))
+        self.meta = AttentionMetadata(self.slots, runner.block_size, plan, None)
+        self.host_meta = self.host[3 * b :].view(torch.int32).numpy()
+        self.host_i64 = self.host[: 3 * b].numpy()
+        self.host_meta[:b] = np.arange(b, dtype=np.int32)
+        self.host_meta[b : 2 * b] = 1
+        self.host_i64[2 * b : 3 * b] = -1  # warm-up rows write no KV slot (kernels skip slot < 0)
+        self.dev.copy_(self.host)
+        model = runner.model
+        stream = torch.cuda.Stream(device=dev)
+        stream.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(stream), torch.inference_mode():
+            for _ in range(2):  # warm-up: reserves every workspace before capture
+                model.compute_logits(model(self.ids, self.pos, runner.kv_caches, self.meta)).argmax(dim=-1)
+        torch.cuda.current_stream(dev).wait_stream(stream)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph), torch.inference_mode():
+            hidden = model(self.ids, self.pos, runner.kv_caches, self.meta)
+            self.out_ids = model.compute_logits(hidden).argmax(dim=-1)
+
+    def run(self, scheduled: list[ScheduledChunk], block_size: int) -> list[int]:
+        b = self.batch
+        for i, s in enumerate(scheduled):
+            p = s.num_computed
+            table = s.block_table
+            self.host_i64[i] = s.token_ids[p]
+            self.host_i64[b + i] = p
+            self.host_i64[2 * b + i] = table[p // block_size] * block_size + p % block_size
+            self.host_meta[b + i] = p + 1
+            need = -(-(p + 1) // block_size)
+            self.host_meta[2 * b + i * self.max_blocks : 2 * b + i * self.max_blocks + need] = table[:need]
+        self.dev.copy_(self.host, non_blocking=True)
+        self.graph.replay()
+        return self.out_ids.tolist()  # the one device -> host sync
+
+
+class ModelRunner:
+    def __init__(
+        self,
+        model: Qwen3ForCausalLM,
+        device: torch.device,
+        dtype: torch.dtype = torch.bfloat16,
+        block_size: int = 16,
+        use_graphs: bool = False,
+        max_model_len: int = 4096,
+    ) -> None:
+        self.model = model
+        self.model_cfg = model.cfg
+        self.device = device
+        self.dtype = dtype
+        self.block_size = block_size
+        self.kv_cache: Tensor | None = None
+        self.kv_caches: list[tuple[Tensor, Tensor]] = []
+        self.num_blocks = 0
+        self.use_graphs = use_graphs
+        self.max_model_len = max_model_len
+        self.graphs: dict[int, CapturedDecode] = {}
+
+    @property
+    def bytes_per_block(self) -> int:
+        return self.model_cfg.kv_bytes_per_token(self.dtype.itemsize) * self.block_size
+
+    def allocate_kv_cache(self, num_blocks: int) -> None:
+        c = self.model_cfg
+        self.kv_cache, self.kv_caches = None, []
+        self.kv_cache = torch.zeros(
+            c.num_hidden_layers, 2, num_blocks * self.block_size, c.num_key_value_heads, c.head_dim,
+            dtype=self.dtype, device=self.device,
+        )
+        self.kv_caches = [(self.kv_cache[i, 0], self.kv_cache[i, 1]) for i in range(c.num_hidden_layers)]
+        self.num_blocks = num_blocks
+        self.graphs = {}  # captured graphs hold the old pool's addresses
+
+    def prepare(self, scheduled: list[ScheduledChunk]) -> StepInputs:
+        """Flatten all scheduled tokens into one batch (model_runner.py:162-205, no speculation)."""
+        bs = self.block_size
+        input_ids: list[int] = []
+        positions: list[int] = []
+        slots: list[int] = []
+        chunks: list[SeqChunk] = []
+        rows: list[int] = []
+        sample_idx: list[int] = []
+        for idx, s in enumerate(scheduled):
+            start, n, table = s.num_computed, s.num_new, s.block_table
+            flat = len(input_ids)
+            input_ids.extend(s.token_ids[start : start + n])
+            positions.extend(range(start, start + n))
+            slots.extend(table[p // bs] * bs + p % bs for p in range(start, start + n))
+            chunks.append(SeqChunk(flat, n, start, table))
+            if start + n == len(s.token_ids):
+                sample_idx.append(idx)
+                rows.append(flat + n - 1)
+        slot_mapping = to_device(slots, self.device)
+        return StepInputs(
+            input_ids=to_device(input_ids, self.device),
+            positions=to_device(positions, self.device),
+            attn=build_attention_metadata(chunks, slot_mapping, bs),
+            logits_rows=to_device(rows, self.device),
+            sample_idx=sample_idx,
+        )
+
+    def _graphable(self, scheduled: list[ScheduledChunk]) -> bool:
+        return all(
+            s.num_new == 1 and s.num_computed + 1 == len(s.token_ids) and s.num_computed < self.max_model_len
+            for s in scheduled
+        )
+
+    @torch.inference_mode()
+    def forward_logits(self, inp: StepInputs) -> Tensor:
+        hidden = self.model(inp.input_ids, inp.positions, self.kv_caches, inp.attn)
+        return self.model.compute_logits(hidden[inp.logits_rows])
+
+    @torch.inference_mode()
+    def execute(self, scheduled: list[ScheduledChunk]) -> list[list[int]]:
+        """Run one step; return each scheduled sequence's new token ids (0 or 1 of them)."""
+        results: list[list[int]] = [[] for _ in scheduled]
+        if not scheduled:
+            return results
+        if self.use_graphs and self._graphable(scheduled):
+            g = self.graphs.get(len(scheduled))
+            if g is None:
+                g = self.graphs[len(scheduled)] = CapturedDecode(self, len(scheduled), self.max_model_len // self.block_size)
+            return [[t] for t in g.run(scheduled, self.block_size)]
+        inp = self.prepare(scheduled)
+        if inp.logits_rows.numel() == 0:
+            self.model(inp.input_ids, inp.positions, self.kv_caches, inp.attn)
+            return results
+        tokens = sample(self.forward_logits(inp)).tolist()  # the one device -> host sync
+        for j, idx in enumerate(inp.sample_idx):
+            results[idx] = [tokens[j]]
+        return results

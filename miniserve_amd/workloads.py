@@ -1,0 +1,144 @@
+"""Seeded synthetic workloads: model geometries, random-init weights, decode/prefill batches and
+KV pools with the shapes the benchmarks and parity tests use.
+
+Everything random is drawn from ``torch.Generator`` on the CPU (so a CPU restatement sees the
+same bits) unless a caller asks for on-device generation of a pool too large to draw on the host.
+Weights: N(0, std) drawn in float32 and rounded to bf16 (the model dtype the reference quantizes
+from); RMSNorm weights 1 (optionally jittered, for tests that must exercise the weight multiply).
+"""
+
+from __future__ import annotations
+
+import random
+from dataclasses import dataclass
+from typing import Any
+
+import torch
+from torch import Tensor
+
+QWEN3_0_6B: dict[str, Any] = {
+    "vocab_size": 151936,
+    "hidden_size": 1024,
+    "intermediate_size": 3072,
+    "num_hidden_layers": 28,
+    "num_attention_heads": 16,
+    "num_key_value_heads": 8,
+    "head_dim": 128,
+    "rms_norm_eps": 1e-6,
+    "rope_theta": 1_000_000.0,
+    "max_position_embeddings": 40960,
+    "tie_word_embeddings": True,
+}
+
+QWEN3_8B: dict[str, Any] = {
+    **QWEN3_0_6B,
+    "hidden_size": 4096,
+    "intermediate_size": 12288,
+    "num_hidden_layers": 36,
+    "num_attention_heads": 32,
+    "num_key_value_heads": 8,
+    "tie_word_embeddings": False,
+}
+
+
+def weight_shapes(cfg: dict[str, Any]) -> dict[str, tuple[int, ...]]:
+    """Parameter name -> shape, in a fixed order, with the fused qkv / gate_up rows."""
+    h, d = cfg["hidden_size"], cfg["head_dim"]
+    q, kv, inter = cfg["num_attention_heads"] * d, cfg["num_key_value_heads"] * d, cfg["intermediate_size"]
+    shapes: dict[str, tuple[int, ...]] = {"embed_tokens.weight": (cfg["vocab_size"], h)}
+    for i in range(cfg["num_hidden_layers"]):
+        p = f"layers.{i}."
+        shapes[p + "input_layernorm.weight"] = (h,)
+        shapes[p + "self_attn.qkv_proj.weight"] = (q + 2 * kv, h)
+        shapes[p + "self_attn.o_proj.weight"] = (h, q)
+        shapes[p + "self_attn.q_norm.weight"] = (d,)
+        shapes[p + "self_attn.k_norm.weight"] = (d,)
+        shapes[p + "post_attention_layernorm.weight"] = (h,)
+        shapes[p + "mlp.gate_up_proj.weight"] = (2 * inter, h)
+        shapes[p + "mlp.down_proj.weight"] = (h, inter)
+    shapes["norm.weight"] = (h,)
+    if not cfg["tie_word_embeddings"]:
+        shapes["lm_head.weight"] = (cfg["vocab_size"], h)
+    return shapes
+
+
+def random_weights(
+    cfg: dict[str, Any], seed: int, std: float = 0.02, norm_jitter: float = 0.0, device: str = "cpu"
+) -> dict[str, Tensor]:
+    """Seeded random-init weights in bf16 (norm weights 1 + norm_jitter * N(0, 1))."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    out: dict[str, Tensor] = {}
+    for name, shape in weight_shapes(cfg).items():
+        if name.endswith("norm.weight"):
+            w = torch.ones(shape, device=device)
+            if norm_jitter:
+                w = w + norm_jitter * torch.randn(shape, generator=g, device=device)
+        else:
+            w = torch.randn(shape, generator=g, device=device) * std
+        out[name] = w.to(torch.bfloat16)
+    return out
+
+
+def build_model(cfg: dict[str, Any], weights: dict[str, Tensor], device: torch.device, max_positions: int):
+    """A bf16 Qwen3ForCausalLM on ``device`` holding ``weights`` (not yet quantized)."""
+    from miniserve_amd.model.qwen3 import Qwen3Config, Qwen3ForCausalLM
+
+    mcfg = Qwen3Config.from_dict(cfg)
+    with torch.device("meta"):
+        model = Qwen3ForCausalLM(mcfg, max_positions)
+    model = model.to_empty(device=device).to(torch.bfloat16)
+    params = dict(model.named_parameters())
+    missing = set(params) - set(weights)
+    if missing:
+        raise ValueError(f"weights are missing {sorted(missing)[:4]}")
+    with torch.no_grad():
+        for name, p in params.items():
+            p.copy_(weights[name].to(device))
+    model.rotary.build(device)
+    return model.eval()
+
+
+@dataclass
+class DecodeBatch:
+    """One decode token per sequence over a paged pool."""
+
+    context_lens: list[int]  # tokens in context INCLUDING this step's token
+    block_tables: list[list[int]]
+    num_blocks: int
+    token_ids: list[int]  # this step's input token per sequence
+
+    @property
+    def slot_mapping(self) -> list[int]:
+        return [t[(c - 1) // 16] * 16 + (c - 1) % 16 for c, t in zip(self.context_lens, self.block_tables, strict=True)]
+
+
+def decode_batch(
+    batch: int, ctx_lo: int, ctx_hi: int, seed: int, vocab: int = 151936, spare_blocks: int = 0
+) -> DecodeBatch:
+    """Contexts uniform in [ctx_lo, ctx_hi]; the pool holds exactly the blocks the batch needs
+    (plus ``spare_blocks``) and each block table is a slice of one random permutation of it."""
+    rng = random.Random(seed)
+    ctx = [rng.randint(ctx_lo, ctx_hi) for _ in range(batch)]
+    need = [-(-c // 16) for c in ctx]
+    total = sum(need) + spare_blocks
+    perm = torch.randperm(total, generator=torch.Generator().manual_seed(seed)).tolist()
+    tables, off = [], 0
+    for n in need:
+        tables.append(perm[off : off + n])
+        off += n
+    ids = [rng.randrange(vocab) for _ in range(batch)]
+    return DecodeBatch(ctx, tables, total, ids)
+
+
+def fill_kv_pool_(kv: Tensor, seed: int, on_device: bool = False) -> None:
+    """Fill a KV pool [layers, 2, slots, KVH, D] (or one [slots, KVH, D] cache) with N(0, 1) bf16,
+    one layer at a time; CPU-generated (bit-reproducible on the host) unless ``on_device``."""
+    views = [kv] if kv.dim() == 3 else [kv[i, j] for i in range(kv.shape[0]) for j in range(kv.shape[1])]
+    if on_device:
+        g = torch.Generator(device=kv.device).manual_seed(seed)
+        for v in views:
+            v.copy_(torch.randn(v.shape, generator=g, device=kv.device, dtype=torch.float32))
+        return
+    g = torch.Generator().manual_seed(seed)
+    for v in views:
+        v.copy_(torch.randn(v.shape, generator=g).to(torch.bfloat16))

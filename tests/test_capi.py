@@ -1,0 +1,83 @@
+"""CPU checks of the C ABI: the library loads next to torch's HIP runtime, exports every entry
+point include/miniserve_amd.h declares with the signatures the ctypes binding uses, and rejects
+bad arguments before launching anything (no GPU needed: these calls fail in host code)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from miniserve_amd import _native
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "miniserve_amd.h"
+
+
+def _declared() -> list[str]:
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\*?(msa_\w+)\(", text, flags=re.M)))
+
+
+def test_header_declares_the_binding():
+    assert _declared() == sorted(_native.SIGNATURES)
+
+
+def test_library_exports_every_symbol():
+    lib = _native.load()
+    for name in _declared():
+        assert getattr(lib, name) is not None
+    assert lib.msa_abi_version() == _native.ABI_VERSION
+
+
+def test_single_hip_runtime_mapped():
+    _native.load()
+    assert len(_native._hip_runtimes_mapped()) <= 1
+
+
+def _err(name, *args):
+    with pytest.raises(RuntimeError) as e:
+        _native.call(name, *args)
+    return str(e.value)
+
+
+NULL = ctypes.c_void_p(0)
+FAKE = ctypes.c_void_p(0x1000)  # never dereferenced: every call below fails validation first
+
+
+def test_argument_errors_are_reported():
+    assert "null pointer" in _err("msa_int8_quantize", NULL, 0, 4, 4, NULL, NULL, NULL)
+    assert "weight_dtype" in _err("msa_int8_quantize", FAKE, 7, 4, 4, FAKE, FAKE, NULL)
+    assert "multiple of 16" in _err(
+        "msa_int8_linear", FAKE, 4, 40, 40, FAKE, FAKE, 32, FAKE, 32, 0, NULL, 0, NULL, 0, NULL
+    )
+    assert "epilogue" in _err("msa_int8_linear", FAKE, 4, 64, 64, FAKE, FAKE, 32, FAKE, 32, 9, NULL, 0, NULL, 0, NULL)
+    assert "head_dim must be 128" in _err(
+        "msa_paged_attention_decode", FAKE, 64, FAKE, FAKE, 16, 2, 1, 64, 16, FAKE, 1, FAKE, FAKE, 1, 16, 1, 1.0,
+        FAKE, 64, NULL, 0, NULL,
+    )
+    assert "block_size must be 16" in _err(
+        "msa_paged_attention_prefill", FAKE, 128, FAKE, FAKE, 16, 2, 1, 128, 8, FAKE, 1, FAKE, FAKE, 1, 1.0, FAKE,
+        128, NULL,
+    )
+    assert "heads / kv_heads" in _err(
+        "msa_paged_attention_prefill", FAKE, 128 * 8, FAKE, FAKE, 16, 8, 1, 128, 16, FAKE, 1, FAKE, FAKE, 1, 1.0,
+        FAKE, 128 * 8, NULL,
+    )
+    assert "head_dim must be even" in _err(
+        "msa_qk_norm_rope_cache", FAKE, 64, 1, 2, 1, 7, FAKE, FAKE, 1e-6, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, NULL
+    )
+
+
+def test_zero_sized_calls_are_no_ops():
+    _native.call("msa_int8_linear", NULL, 0, 64, 64, NULL, NULL, 32, NULL, 32, 0, NULL, 0, NULL, 0, NULL)
+    _native.call("msa_rmsnorm", NULL, 64, NULL, NULL, 64, 0, 64, 1e-6, NULL)
+
+
+def test_workspace_sizes():
+    assert _native.query("msa_int8_linear_workspace_size", 1, 1024, 64) == 0  # one K chunk per wave: no split
+    assert _native.query("msa_int8_linear_workspace_size", 64, 1024, 2048) > 0
+    assert _native.query("msa_paged_attention_decode_workspace_size", 64, 16, 128, 1) == 0
+    ws = _native.query("msa_paged_attention_decode_workspace_size", 64, 16, 128, 8)
+    assert ws >= 64 * 16 * 8 * (128 + 2) * 4

@@ -1,0 +1,346 @@
+"""GPU parity of each HIP kernel against the CPU oracle on the same seeded inputs.
+
+Bars: int8 packing bit-exact; linears within rel-L2 1e-2 of the oracle (and within bf16 rounding
+of a float64 product of the same dequantized weights); norms / RoPE / cache writes bit-exact but
+for the order of a float32 sum; attention within rel-L2 1e-2 of the oracle's SDPA path (and of a
+float64 brute force). Every call goes through the C ABI of libminiserve_amd.so.
+"""
+
+from __future__ import annotations
+
+import random
+
+import pytest
+import torch
+from helpers import rel_l2
+
+from miniserve_amd import kernels
+from miniserve_amd.attention import backends as hb
+from oracle import attention as oa
+from oracle import int8 as oi
+from oracle import layers as ol
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+def _bf16(shape, seed, std=1.0):
+    return (torch.randn(shape, generator=torch.Generator().manual_seed(seed)) * std).to(torch.bfloat16)
+
+
+# ---- int8 pack ------------------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("shape", [(3072, 1024), (4096, 1024), (1024, 3072), (7, 48), (130, 4096)])
+def test_quantize_bit_exact(shape):
+    w = _bf16(shape, seed=shape[0], std=0.02)
+    w[min(3, shape[0] - 1)] = 0  # an all-zero row
+    q, s = kernels.int8_quantize(w.to(DEV))
+    qo, so = oi.quantize_int8(w)
+    assert torch.equal(q.cpu(), qo)
+    assert torch.equal(s.cpu().view(torch.int16), so.view(torch.int16))
+
+
+def test_quantize_ties_and_float32_input():
+    row = torch.tensor([[127.0, 2.5, -2.5, 3.5, 0.5, -0.5, 1.5, -126.5] * 2], dtype=torch.float32)
+    q, s = kernels.int8_quantize(row.to(DEV))
+    assert q.cpu().tolist() == [[127, 2, -2, 4, 0, 0, 2, -126] * 2]
+    w = torch.randn(64, 96, generator=torch.Generator().manual_seed(3)) * 0.05
+    q, s = kernels.int8_quantize(w.to(DEV))
+    qo, so = oi.quantize_int8(w)
+    assert torch.equal(q.cpu(), qo)
+    assert torch.equal(s.cpu().view(torch.int16), so.to(torch.bfloat16).view(torch.int16))
+
+
+# ---- int8 linear ----------------------------------------------------------------------------------
+
+LINEAR_SHAPES = [
+    (16, 3072, 1024),  # gate_proj-shaped single linear at M=16
+    (64, 4096, 1024),  # qkv
+    (64, 1024, 2048),  # o
+    (64, 1024, 3072),  # down
+    (1, 4096, 1024),
+    (5, 1024, 2048),
+    (33, 512, 256),
+    (100, 1024, 1024),  # two 64-row chunks
+    (256, 1024, 512),
+    (3, 48, 80),  # ragged: n not a multiple of 32, k of 64
+]
+
+
+def _linear_inputs(m, n, k, seed):
+    w = _bf16((n, k), seed, std=0.02)
+    q, s = oi.quantize_int8(w)
+    x = _bf16((m, k), seed + 1)
+    return x, q, s
+
+
+def _deq64(q, s):
+    return q.double() * s.double()[:, None]
+
+
+@pytest.mark.parametrize("m,n,k", LINEAR_SHAPES + LINEAR_SHAPES[::-1])
+def test_linear_parity(m, n, k):
+    x, q, s = _linear_inputs(m, n, k, seed=m * 7 + n)
+    y = kernels.int8_linear(x.to(DEV), q.to(DEV), s.to(DEV))
+    y2 = kernels.int8_linear(x.to(DEV), q.to(DEV), s.to(DEV))  # counters were reset by the first call
+    ref = oi.int8_linear(x, q, s)
+    exact = x.double() @ oi.dequantize(q, s, torch.bfloat16).double().T
+    assert y.shape == (m, n) and y.dtype == torch.bfloat16
+    assert torch.equal(y, y2)
+    assert rel_l2(y.cpu(), ref) < 1e-2
+    assert rel_l2(y.cpu(), exact) < 4e-3
+
+
+@pytest.mark.parametrize("m", [1, 16, 64, 77])
+def test_linear_silu_mul_epilogue(m):
+    n, k = 6144, 1024
+    x, q, s = _linear_inputs(m, n, k, seed=m)
+    y = kernels.int8_linear(x.to(DEV), q.to(DEV), s.to(DEV), epilogue=kernels.EPI_SILU_MUL)
+    gate, up = oi.int8_linear(x, q, s).chunk(2, dim=-1)
+    ref = torch.nn.functional.silu(gate) * up
+    assert y.shape == (m, n // 2)
+    assert rel_l2(y.cpu(), ref) < 1e-2
+
+
+@pytest.mark.parametrize("m", [1, 64])
+def test_linear_residual_epilogue(m):
+    n, k = 1024, 3072
+    x, q, s = _linear_inputs(m, n, k, seed=11 + m)
+    r = _bf16((m, n), seed=12)
+    y = kernels.int8_linear(x.to(DEV), q.to(DEV), s.to(DEV), epilogue=kernels.EPI_RESIDUAL, residual=r.to(DEV))
+    ref = r + oi.int8_linear(x, q, s)
+    assert rel_l2(y.cpu(), ref) < 1e-2
+
+
+def test_linear_rejects_bad_shapes():
+    q = torch.zeros(32, 40, dtype=torch.int8, device=DEV)
+    s = torch.ones(32, dtype=torch.bfloat16, device=DEV)
+    x = torch.zeros(4, 40, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(RuntimeError, match="multiple of 16"):
+        kernels.int8_linear(x, q, s)
+
+
+# ---- norms / rope / cache -------------------------------------------------------------------------
+
+
+def _close_bf16(got, ref, frac=0.02, scale=None):
+    """Equal except where the float32 sum order moved an intermediate by one bf16 step: at most
+    one step of ``scale`` (the magnitude the last rounding saw; default the value itself), and
+    only in a small fraction of the elements."""
+    diff = (got.float() - ref.float()).abs()
+    mag = ref.float().abs() if scale is None else scale.float().abs()
+    ulp = mag.clamp_min(1e-30) * 2.0**-7
+    assert torch.all(diff <= ulp * 1.01 + 1e-30), float((diff / ulp).max())
+    assert float((diff > 0).float().mean()) <= frac
+    assert rel_l2(got, ref) < 1e-3
+
+
+@pytest.mark.parametrize("rows,dim", [(64, 1024), (3, 4096), (5, 64)])
+def test_rmsnorm(rows, dim):
+    x = _bf16((rows, dim), seed=dim)
+    w = (1 + 0.1 * torch.randn(dim, generator=torch.Generator().manual_seed(1))).to(torch.bfloat16)
+    y = kernels.rmsnorm(x.to(DEV), w.to(DEV), 1e-6)
+    _close_bf16(y.cpu(), ol.rms_norm(x, w, 1e-6))
+
+
+def test_add_rmsnorm():
+    x = _bf16((64, 1024), seed=1)
+    d = _bf16((64, 1024), seed=2)
+    w = (1 + 0.1 * torch.randn(1024, generator=torch.Generator().manual_seed(3))).to(torch.bfloat16)
+    r, y = kernels.add_rmsnorm(x.to(DEV), d.to(DEV), w.to(DEV), 1e-6)
+    assert torch.equal(r.cpu(), x + d)
+    _close_bf16(y.cpu(), ol.rms_norm(x + d, w, 1e-6))
+
+
+@pytest.mark.parametrize("heads,kv_heads,dim", [(16, 8, 128), (32, 8, 128), (4, 2, 16)])
+def test_qk_norm_rope_cache(heads, kv_heads, dim):
+    t, slots_total = 37, 160
+    qkv = _bf16((t, (heads + 2 * kv_heads) * dim), seed=heads)
+    gen = torch.Generator().manual_seed(5)
+    qw = (1 + 0.1 * torch.randn(dim, generator=gen)).to(torch.bfloat16)
+    kw = (1 + 0.1 * torch.randn(dim, generator=gen)).to(torch.bfloat16)
+    cos_t, sin_t = ol.rope_tables(dim, 4096, 1e6)
+    pos = torch.randint(0, 4096, (t,), generator=gen)
+    slots = torch.randperm(slots_total, generator=gen)[:t]
+    kc = torch.zeros(slots_total, kv_heads, dim, dtype=torch.bfloat16)
+    vc = torch.zeros_like(kc)
+    kcg, vcg = kc.to(DEV), vc.to(DEV)
+    q = kernels.qk_norm_rope_cache(
+        qkv.to(DEV), heads, kv_heads, dim, qw.to(DEV), kw.to(DEV), 1e-6, cos_t[pos].to(DEV), sin_t[pos].to(DEV),
+        slots.to(DEV), kcg, vcg,
+    )
+    qr, kr, vr = qkv.split([heads * dim, kv_heads * dim, kv_heads * dim], dim=-1)
+    qn = ol.rms_norm(qr.reshape(t, heads, dim), qw, 1e-6)
+    kn = ol.rms_norm(kr.reshape(t, kv_heads, dim), kw, 1e-6)
+    qo, ko = ol.apply_rope(qn, kn, cos_t[pos], sin_t[pos])
+    # RoPE sums two rounded products: a one-step change of the normed input can move the
+    # (possibly cancelling) sum by one step of the larger product's magnitude.
+    qmag = qn.float().abs() + torch.cat([qn[..., dim // 2 :], qn[..., : dim // 2]], -1).float().abs()
+    kmag = kn.float().abs() + torch.cat([kn[..., dim // 2 :], kn[..., : dim // 2]], -1).float().abs()
+    _close_bf16(q.cpu(), qo, scale=qmag)
+    _close_bf16(kcg.cpu()[slots], ko, scale=kmag)
+    assert torch.equal(vcg.cpu()[slots], vr.reshape(t, kv_heads, dim))
+    untouched = torch.ones(slots_total, dtype=torch.bool)
+    untouched[slots] = False
+    assert torch.all(kcg.cpu()[untouched] == 0) and torch.all(vcg.cpu()[untouched] == 0)
+
+
+def test_reshape_and_cache():
+    t, kvh, d, n = 21, 8, 128, 64
+    k, v = _bf16((t, kvh, d), 1), _bf16((t, kvh, d), 2)
+    slots = torch.randperm(n, generator=torch.Generator().manual_seed(3))[:t]
+    kc = torch.zeros(n, kvh, d, dtype=torch.bfloat16, device=DEV)
+    vc = torch.zeros_like(kc)
+    kernels.reshape_and_cache(k.to(DEV), v.to(DEV), kc, vc, slots.to(DEV))
+    assert torch.equal(kc.cpu()[slots], k) and torch.equal(vc.cpu()[slots], v)
+
+
+# ---- paged attention ------------------------------------------------------------------------------
+
+
+def _attention_case(specs, heads, kv_heads, seed, dim=128, spare=3):
+    """specs: (num_cached, num_new) per sequence. Random permuted block tables over one pool."""
+    bs = 16
+    rng = random.Random(seed)
+    g = torch.Generator().manual_seed(seed)
+    need = sum(-(-(c + n) // bs) for c, n in specs)
+    nblocks = need + spare
+    perm = list(range(nblocks))
+    rng.shuffle(perm)
+    chunks, slots, flat, used = [], [], 0, 0
+    for cached, new in specs:
+        nb = -(-(cached + new) // bs)
+        table = perm[used : used + nb]
+        used += nb
+        chunks.append((flat, new, cached, table))
+        slots.extend(table[p // bs] * bs + p % bs for p in range(cached, cached + new))
+        flat += new
+    q = torch.randn(flat, heads, dim, generator=g).to(torch.bfloat16)
+    k = torch.randn(flat, kv_heads, dim, generator=g).to(torch.bfloat16)
+    v = torch.randn(flat, kv_heads, dim, generator=g).to(torch.bfloat16)
+    kc = torch.randn(nblocks * bs, kv_heads, dim, generator=g).to(torch.bfloat16)
+    vc = torch.randn(nblocks * bs, kv_heads, dim, generator=g).to(torch.bfloat16)
+    return q, k, v, kc, vc, chunks, torch.tensor(slots, dtype=torch.long)
+
+
+def _run_both(specs, heads, kv_heads, seed):
+    q, k, v, kc, vc, chunks, slots = _attention_case(specs, heads, kv_heads, seed)
+    scale = 128**-0.5
+    ometa = oa.build_attention_metadata([oa.SeqChunk(*c) for c in chunks], slots, 16)
+    kco, vco = kc.clone(), vc.clone()
+    ref = oa.paged_attention(q, k, v, kco, vco, ometa, scale)
+    kcg, vcg = kc.to(DEV), vc.to(DEV)
+    hmeta = hb.build_attention_metadata([hb.SeqChunk(*c) for c in chunks], slots.to(DEV), 16)
+    out = hb.paged_attention(q.to(DEV), k.to(DEV), v.to(DEV), kcg, vcg, hmeta, scale)
+    assert torch.equal(kcg.cpu(), kco) and torch.equal(vcg.cpu(), vco)
+    dense = oa.dense_attention(q, kco, vco, [oa.SeqChunk(*c) for c in chunks], 16, scale)
+    return out.cpu(), ref, dense
+
+
+@pytest.mark.parametrize("heads,kv_heads", [(16, 8), (32, 8), (8, 8), (64, 8)])
+def test_decode_attention(heads, kv_heads):
+    rng = random.Random(heads)
+    specs = [(rng.randint(0, 700), 1) for _ in range(23)] + [(0, 1), (15, 1), (16, 1), (2047, 1)]
+    out, ref, dense = _run_both(specs, heads, kv_heads, seed=heads)
+    assert rel_l2(out, ref) < 1e-2
+    assert rel_l2(out, dense) < 1e-2
+
+
+def test_decode_attention_config2_shape():
+    """64 sequences, contexts uniform in [128, 2048], 16 q / 8 kv heads, permuted blocks."""
+    rng = random.Random(2)
+    specs = [(rng.randint(128, 2048) - 1, 1) for _ in range(64)]
+    out, ref, _ = _run_both(specs, 16, 8, seed=2)
+    assert rel_l2(out, ref) < 1e-2
+    for i in (0, 31, 63):
+        assert rel_l2(out[i], ref[i]) < 1e-2
+
+
+@pytest.mark.parametrize("heads,kv_heads", [(16, 8), (32, 8), (8, 8)])
+def test_prefill_attention(heads, kv_heads):
+    # fresh prompts, a chunk after cached keys, speculative-verify-sized rows, ragged tiles
+    specs = [(0, 200), (37, 100), (64, 3), (5, 8), (0, 2), (300, 33), (0, 17)]
+    out, ref, dense = _run_both(specs, heads, kv_heads, seed=heads + 1)
+    assert rel_l2(out, ref) < 1e-2
+    assert rel_l2(out, dense) < 1e-2
+
+
+def test_mixed_decode_and_prefill_batch():
+    """Decodes first, then one long fresh chunk -- the chunked-prefill step's flat order."""
+    rng = random.Random(4)
+    specs = [(rng.randint(64, 1024) - 1, 1) for _ in range(16)] + [(0, 500)]
+    out, ref, _ = _run_both(specs, 16, 8, seed=4)
+    assert rel_l2(out, ref) < 1e-2
+    assert rel_l2(out[:16], ref[:16]) < 1e-2
+
+
+# ---- split-K linears and the kernels that consume their partials --------------------------------
+
+
+@pytest.mark.parametrize("m,n,k,split", [(64, 1024, 2048, 8), (64, 1024, 3072, 6), (5, 4096, 1024, 2), (64, 256, 64, 1)])
+def test_linear_splitk_partials(m, n, k, split):
+    x, q, s = _linear_inputs(m, n, k, seed=n + split)
+    part = kernels.int8_linear_splitk(x.to(DEV), q.to(DEV), s.to(DEV), split)
+    assert part.shape == (split, m, n) and part.dtype == torch.float32
+    y = part.cpu().sum(0).to(torch.bfloat16)
+    exact = x.double() @ oi.dequantize(q, s, torch.bfloat16).double().T
+    assert rel_l2(y, oi.int8_linear(x, q, s)) < 1e-2
+    assert rel_l2(part.cpu().double().sum(0), exact) < 1e-5  # float32 sums of the same products
+
+
+def test_splitk_add_rmsnorm_matches_unfused():
+    m, n, k = 64, 1024, 2048
+    x, q, s = _linear_inputs(m, n, k, seed=21)
+    resid = _bf16((m, n), seed=22)
+    w = (1 + 0.1 * torch.randn(n, generator=torch.Generator().manual_seed(23))).to(torch.bfloat16)
+    part = kernels.int8_linear_splitk(x.to(DEV), q.to(DEV), s.to(DEV), 2)
+    xo, h = kernels.splitk_add_rmsnorm(part, resid.to(DEV), w.to(DEV), 1e-6)
+    delta = (part[0] + part[1]).to(torch.bfloat16).cpu()  # two splits: one addition, same order
+    assert torch.equal(xo.cpu(), resid + delta)
+    _close_bf16(h.cpu(), ol.rms_norm(resid + delta, w, 1e-6))
+    # and against the oracle's linear + add + norm, within bf16 noise
+    ref_x = resid + oi.int8_linear(x, q, s)
+    assert rel_l2(xo.cpu(), ref_x) < 1e-2
+
+
+def test_qk_norm_rope_cache_splitk_matches_unfused():
+    heads, kvh, dim, t, k = 16, 8, 128, 19, 1024
+    n = (heads + 2 * kvh) * dim
+    x, q, s = _linear_inputs(t, n, k, seed=31)
+    part = kernels.int8_linear_splitk(x.to(DEV), q.to(DEV), s.to(DEV), 2)
+    qkv = (part[0] + part[1]).to(torch.bfloat16)
+    gen = torch.Generator().manual_seed(32)
+    qw = (1 + 0.1 * torch.randn(dim, generator=gen)).to(torch.bfloat16).to(DEV)
+    kw = (1 + 0.1 * torch.randn(dim, generator=gen)).to(torch.bfloat16).to(DEV)
+    cos_t, sin_t = ol.rope_tables(dim, 512, 1e6)
+    pos = torch.randint(0, 512, (t,), generator=gen)
+    cs, sn = cos_t[pos].to(DEV), sin_t[pos].to(DEV)
+    slots = torch.randperm(64, generator=gen)[:t].to(DEV)
+    caches = [torch.zeros(64, kvh, dim, dtype=torch.bfloat16, device=DEV) for _ in range(4)]
+    qa = kernels.qk_norm_rope_cache_splitk(part, heads, kvh, dim, qw, kw, 1e-6, cs, sn, slots, caches[0], caches[1])
+    qb = kernels.qk_norm_rope_cache(qkv, heads, kvh, dim, qw, kw, 1e-6, cs, sn, slots, caches[2], caches[3])
+    assert torch.equal(qa, qb)
+    assert torch.equal(caches[0], caches[2]) and torch.equal(caches[1], caches[3])
+
+
+@pytest.mark.parametrize("heads,kv_heads,ptok", [(16, 8, 64), (32, 8, 128), (16, 8, 16)])
+def test_decode_attention_split_across_workgroups(heads, kv_heads, ptok):
+    """Force the workgroup-level split (workspace + merge kernel) that small batches use."""
+    rng = random.Random(ptok)
+    specs = [(rng.randint(0, 900), 1) for _ in range(5)] + [(0, 1), (ptok - 1, 1), (ptok, 1)]
+    q, k, v, kc, vc, chunks, slots = _attention_case(specs, heads, kv_heads, seed=ptok)
+    scale = 128**-0.5
+    ref = oa.paged_attention(q, k, v, kc.clone(), vc.clone(),
+                             oa.build_attention_metadata([oa.SeqChunk(*c) for c in chunks], slots, 16), scale)
+    kcg, vcg = kc.to(DEV), vc.to(DEV)
+    kernels.reshape_and_cache(k.to(DEV), v.to(DEV), kcg, vcg, slots.to(DEV))
+    meta = hb.build_attention_metadata([hb.SeqChunk(*c) for c in chunks], slots.to(DEV), 16)
+    d = meta.decode
+    parts = -(-d.block_tables.shape[1] * 16 // ptok)
+    out = torch.zeros(q.shape, dtype=torch.bfloat16, device=DEV)
+    for _ in range(2):  # the workspace is reused as is: nothing needs clearing between calls
+        kernels.paged_attention_decode(q.to(DEV), kcg, vcg, d.block_tables, d.context_lens, d.q_rows, ptok, parts,
+                                       scale, out)
+        assert rel_l2(out.cpu(), ref) < 1e-2
+    assert kernels.decode_splits(2, 8, 256)[1] > 1  # the host picks splits for small batches
