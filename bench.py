@@ -74,13 +74,87 @@ def time_attention(runner, sched, cfg, reps: int = 4) -> tuple[float, int]:
     return sum(spans) / len(spans), attention_bytes(ctx, heads, kvh, dim)
 
 
+def linear_bytes(m: int, n: int, k: int) -> int:
+    """Algorithmic bytes of one int8 linear: int8 weights, bf16 scales, bf16 x in, bf16 y out."""
+    return n * k + 2 * n + 2 * m * k + 2 * m * n
+
+
+def time_linears(seed: int) -> list[dict]:
+    """Average duration of the token-split int8 linear on the single gate_proj-shaped linear
+    ([3072 x 1024], 16 tokens) and on the four decode-step linears at 64 tokens, each over enough
+    distinct weight copies (> 256 MiB) that the Infinity Cache cannot serve repeats; HIP events on
+    the launch stream around one pass over the copies, after a warm-up pass."""
+    import torch
+
+    from miniserve_amd import kernels
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(seed)
+    shapes = [("gate_proj [3072x1024], 16 tokens", 16, 3072, 1024, kernels.EPI_NONE),
+              ("qkv [4096x1024] + q/k-norm/RoPE/cache, 64 tokens", 64, 4096, 1024, -1),
+              ("o [1024x2048] + residual, 64 tokens", 64, 1024, 2048, kernels.EPI_RESIDUAL),
+              ("gate_up [6144x1024] + norm + silu*up, 64 tokens", 64, 6144, 1024, kernels.EPI_SILU_MUL),
+              ("down [1024x3072] + residual, 64 tokens", 64, 1024, 3072, kernels.EPI_RESIDUAL)]
+    out = []
+    for name, m, n, k, epi in shapes:
+        copies = max(8, -(-(300 << 20) // (n * k)))
+        ws = torch.randint(-127, 128, (copies, n, k), dtype=torch.int8, device=dev, generator=g)
+        sc = (torch.rand(copies, n, device=dev, generator=g) * 0.001).to(torch.bfloat16)
+        x = torch.randn(m, k, device=dev, generator=g).to(torch.bfloat16)
+        nw = torch.ones(k, dtype=torch.bfloat16, device=dev)
+        resid = torch.randn(m, n, device=dev, generator=g).to(torch.bfloat16)
+        y = torch.empty(m, n // 2 if epi == kernels.EPI_SILU_MUL else n, dtype=torch.bfloat16, device=dev)
+        if epi == -1:
+            heads, kvh = 16, 8
+            pos = torch.arange(m, device=dev) + 300
+            cos = torch.randn(4096, 128, device=dev)
+            sin = torch.randn(4096, 128, device=dev)
+            slots = torch.arange(m, device=dev)
+            kc = torch.zeros(m, kvh, 128, dtype=torch.bfloat16, device=dev)
+            vc = torch.zeros_like(kc)
+
+            def run(i):
+                kernels.qkv_rope_cache_rows(x, ws[i], sc[i], heads, kvh, 128, nw[:128], nw[:128], 1e-6, pos, cos, sin,
+                                            slots, kc, vc, norm_w=nw, eps=1e-6)
+        elif epi == kernels.EPI_SILU_MUL:
+            def run(i):
+                kernels.int8_linear_rows(x, ws[i], sc[i], epi, norm_w=nw, eps=1e-6, out=y)
+        elif epi == kernels.EPI_RESIDUAL:
+            def run(i):
+                kernels.int8_linear_rows(x, ws[i], sc[i], epi, residual=resid, out=y)
+        else:
+            def run(i):
+                kernels.int8_linear_rows(x, ws[i], sc[i], out=y)
+        for i in range(copies):
+            run(i)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(5_000_000)
+        e0.record()
+        for i in range(copies):
+            run(i)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / copies
+        nbytes = linear_bytes(m, n, k)
+        out.append({"linear": name, "us_per_launch": round(us, 3), "bytes_per_launch": nbytes,
+                    "GB_s": round(nbytes / us / 1e3, 1), "copies": copies})
+        del ws, sc
+    return out
+
+
 def kernel_only(mode: str, seed: int) -> int:
     """Profiling entry points: ``attention`` runs only the decode-attention timing above on the
-    bench workload; ``copy`` copies a 256 MiB buffer 10 times (a kernel of known traffic, to
-    calibrate rocprofv3's FETCH_SIZE / WRITE_SIZE counters)."""
+    bench workload; ``linear`` the int8 linear timings of ``time_linears``; ``copy`` copies a
+    256 MiB buffer 10 times (a kernel of known traffic, to calibrate rocprofv3's FETCH_SIZE /
+    WRITE_SIZE counters)."""
     import torch
 
     dev = torch.device("cuda:0")
+    if mode == "linear":
+        for row in time_linears(seed):
+            print(json.dumps(row))
+        return 0
     if mode == "copy":
         src = torch.empty(128 << 20, dtype=torch.bfloat16, device=dev).normal_()
         dst = torch.empty_like(src)
@@ -115,7 +189,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--kernel-only", choices=["attention", "copy"], help="profiling entry point (see kernel_only)")
+    ap.add_argument("--kernel-only", choices=["attention", "linear", "copy"], help="profiling entry point (see kernel_only)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)

@@ -73,6 +73,50 @@ int msa_int8_linear_splitk(const uint16_t* x, int64_t m, int64_t k, int64_t ldx,
                            const uint16_t* scale, int64_t n, int k_split, float* partials,
                            msa_stream_t stream);
 
+/* Int8Linear.forward (quant/int8.py:35-37) for decode-sized batches, split over tokens instead of
+ * K: a workgroup owns up to 16 tokens x a block of weight rows over the whole of K, so there are
+ * no float32 partials. Epilogues as msa_int8_linear (MSA_EPI_RESIDUAL may write y in place over
+ * residual). With MSA_EPI_SILU_MUL an RMSNorm prologue may be applied to the activations (norm_w
+ * non-NULL; model/layers.py:18-22 with eps), as when gate_up consumes post_attention_layernorm
+ * (model/qwen3.py:122); other epilogues take norm_w = NULL. k % 64 == 0 and
+ * 16 * (k + 8) * 2 bytes + 16 KiB <= 160 KiB (k <= 4416); x, qweight, norm_w 16-byte aligned. */
+int msa_int8_linear_rows(const uint16_t* x, int64_t ldx, int64_t m, int64_t k, const uint16_t* norm_w, float eps,
+                         const int8_t* qweight, const uint16_t* scale, int64_t n, int epilogue, uint16_t* y,
+                         int64_t ldy, const uint16_t* residual, int64_t ldr, msa_stream_t stream);
+
+/* The front half of Qwen3Attention.forward (model/qwen3.py:94-98) plus the cache write of
+ * paged_attention (attention/backends.py:159-160), fused with the layer's input RMSNorm
+ * (model/qwen3.py:121) and, for the first layer, the embedding lookup (model/qwen3.py:148):
+ * activation rows are x[gather_rows[t]] when gather_rows is non-NULL (then also copied to x_copy:
+ * the residual stream; indices are clamped into [0, x_rows)) else x[t]; RMSNorm with norm_w when non-NULL; int8 qkv projection (rows
+ * [q | k | v], model/loader.py:22-28); per-head RMSNorm of q and k (q_norm_w / k_norm_w, qk_eps);
+ * RoPE at positions[t] from the float32 tables [max_positions, 128] (model/layers.py:43-65);
+ * q -> q_out [tokens, heads, 128]; k, v -> k_cache / v_cache [num_slots, kv_heads, 128] at
+ * slot_mapping[t] (slots outside [0, num_slots) are not written). head_dim == 128. */
+int msa_qkv_rope_cache_rows(const uint16_t* x, int64_t ldx, int64_t x_rows, const int64_t* gather_rows,
+                            const uint16_t* norm_w,
+                            float eps, uint16_t* x_copy, int64_t ld_copy, int64_t tokens, int64_t hidden,
+                            const int8_t* qweight, const uint16_t* scale, int heads, int kv_heads, int head_dim,
+                            const uint16_t* q_norm_w, const uint16_t* k_norm_w, float qk_eps,
+                            const int64_t* positions, const float* cos_table, const float* sin_table,
+                            int64_t max_positions, const int64_t* slot_mapping, uint16_t* q_out,
+                            uint16_t* k_cache, uint16_t* v_cache, int64_t num_slots, msa_stream_t stream);
+
+/* Bytes of workspace msa_lm_head_argmax needs (per-row-block argmax candidates). */
+size_t msa_lm_head_argmax_workspace_size(int64_t num_rows, int64_t vocab);
+
+/* Final norm + LM head + greedy sampling (model/qwen3.py:152-158, runner/model_runner.py:217,
+ * runner/sampler.py:59) without materializing logits: for each i < num_rows,
+ * out_ids[i] = argmax_v bf16(RMSNorm(hidden[rows[i]]) . weight[v]) (rows[i] clamped into
+ * [0, hidden_rows)) with the first index winning
+ * ties -- the argmax of the reference's bf16 logits cast to float32. norm_w NULL: the rows are
+ * taken as already normalized. weight [vocab, k] bf16 (the tied embedding or the LM head).
+ * k % 32 == 0. */
+int msa_lm_head_argmax(const uint16_t* hidden, int64_t ld_hidden, int64_t hidden_rows, const int64_t* rows,
+                       int64_t num_rows, int64_t k,
+                       const uint16_t* norm_w, float eps, const uint16_t* weight, int64_t vocab, int64_t* out_ids,
+                       void* workspace, size_t workspace_bytes, msa_stream_t stream);
+
 /* ---- norms, RoPE and the KV-cache write (model/layers.py, model/qwen3.py) -------------------- */
 
 /* RMSNorm.forward (model/layers.py:18-22): out = bf16(w * bf16(x * rsqrt(mean(x^2) + eps))). */

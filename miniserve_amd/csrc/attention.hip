@@ -1,15 +1,13 @@
 // Paged attention over the slot pool [num_slots, KVH, D] (slot = block * 16 + offset), GQA with
 // query head h reading KV head h / (H / KVH), scale applied to q.k, softmax over the visible keys.
 //
-// Decode (one new token per sequence): a workgroup of eight wavefronts per (sequence, KV head);
-// the wavefronts interleave the sequence's 16-token blocks. A 256-byte key/value row (128 bf16) is
-// read by 16 lanes with 16-byte loads, four token rows per load instruction, straight from the
-// pool through the block table -- no gathered copy. The G = H / KVH query heads of the KV head
-// share every K/V load. Dot products are float32 FMAs reduced over the 16 lanes with DPP; the
-// online softmax keeps (max, sum, acc) per lane, merges the four token rows at the end, then the
-// wavefronts through LDS. Only when sequences x KV heads are too few to fill the GPU does the host
-// add workgroup-level splits; those write (acc, max, sum) to a workspace and a second small
-// kernel merges them -- no workgroup ever waits for another.
+// Decode (one new token per sequence): a workgroup of four wavefronts per (sequence, KV head);
+// the wavefronts interleave the sequence's 16-token blocks, read straight from the pool through
+// the block table -- no gathered copy. The G = H / KVH query heads of the KV head share every K/V
+// load. The arithmetic runs on bf16 pairs with v_dot2_f32_bf16 (the kernel is otherwise bound by
+// VALU issue, not HBM); the wavefronts merge through LDS. Only when sequences x KV heads are too
+// few to fill the GPU does the host add workgroup-level splits; those write (acc, max, sum) to a
+// workspace and a second small kernel merges them -- no workgroup ever waits for another.
 //
 // Prefill (any number of new tokens, fresh or after cached keys): flash-attention on MFMA. A
 // workgroup of four wavefronts owns one KV head and 64 / G query tokens; wavefront w takes query
@@ -62,9 +60,42 @@ __device__ __forceinline__ int decode_context(const DecodeArgs& a, int seq) {
 }
 
 // Workgroup = W wavefronts for one (sequence, KV head, split). Wave w takes blocks b0 + w,
-// b0 + w + W, ... of the split, keeping one block of K and V in flight ahead of the one it
-// computes. Lane (r, c) = (lane / 16, lane % 16) owns dims 8c..8c+7 of token rows r, r+4, r+8,
-// r+12 of each block. The waves meet in LDS at the end.
+// b0 + w + W, ... of the split, keeping the next block's K and V in flight while it computes one.
+//
+// Lane (rp, dg) = (lane / 8, lane % 8) owns key rows 2rp and 2rp + 1 of each 16-token block and
+// dims [8dg, 8dg + 8) and [64 + 8dg, 64 + 8dg + 8) of each row: one load instruction covers the
+// same 128 contiguous bytes of eight rows. bf16 pairs are multiplied with v_dot2_f32_bf16 (exact
+// products, float32 sums): q.k takes 8 dot2 per (row, head) plus a 3-step DPP sum over the 8
+// lanes of the row; p.v pairs the two rows' values of each dim with v_perm and takes 16 dot2 per
+// head, with p rounded to bf16 as the MFMA prefill path does. The running maximum of each head is
+// wave-uniform (the accumulators are rescaled only when it grows); sums and accumulators are
+// lane-local (this lane's rows) and merged over the row pairs, then the wavefronts, at the end.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+// Sum over the 8 lanes of an aligned 8-lane group (quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror).
+__device__ __forceinline__ float group8_sum(float v) {
+  v += dpp<0xB1>(v);
+  v += dpp<0x4E>(v);
+  v += dpp<0x141>(v);
+  return v;
+}
+// Across the 8 row-pair groups of a wavefront (values are uniform within each 8-lane group).
+__device__ __forceinline__ float rowpair_max(float v) {
+  v = fmaxf(v, dpp<0x140>(v));  // row_mirror: group g <-> the other group of its 16-lane row
+  v = fmaxf(v, __shfl_xor(v, 16));
+  v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+__device__ __forceinline__ float rowpair_sum(float v) {
+  v += __shfl_xor(v, 8);
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+
 template <int G, int W>
 __global__ __launch_bounds__(64 * W) void paged_decode_kernel(DecodeArgs a) {
   __shared__ float s_acc[W][G][kHeadDim];
@@ -75,117 +106,130 @@ __global__ __launch_bounds__(64 * W) void paged_decode_kernel(DecodeArgs a) {
   if (start >= ctx) return;  // the reduce kernel merges only splits that hold keys
   const int end = min(ctx, start + a.part_tokens);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int r = lane >> 4, c = lane & 15;
+  const int rp = lane >> 3, dg = lane & 7;
   const int64_t qrow = a.qrows[seq];
 
-  float qf[G][8];
+  // q of this lane's 16 dims for each head of the group, as bf16 pairs
+  uint32_t qv[G][8];
 #pragma unroll
   for (int h = 0; h < G; ++h) {
-    const uint4 v = *(const uint4*)(a.q + qrow * a.ldq + (int64_t)(kvh * G + h) * kHeadDim + c * 8);
-    unpack8(v, qf[h]);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) qf[h][e] *= a.scale_log2;
+    const uint16_t* qp = a.q + qrow * a.ldq + (int64_t)(kvh * G + h) * kHeadDim + 8 * dg;
+    const uint4 lo = *(const uint4*)qp, hi = *(const uint4*)(qp + 64);
+    qv[h][0] = lo.x; qv[h][1] = lo.y; qv[h][2] = lo.z; qv[h][3] = lo.w;
+    qv[h][4] = hi.x; qv[h][5] = hi.y; qv[h][6] = hi.z; qv[h][7] = hi.w;
   }
-  float m[G], l[G], acc[G][8];
+  float m[G], l[G], acc[G][16];
 #pragma unroll
   for (int h = 0; h < G; ++h) {
     m[h] = -INFINITY;
     l[h] = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
+    for (int e = 0; e < 16; ++e) acc[h][e] = 0.f;
   }
 
   const int b1 = (end + kBlock - 1) / kBlock;
   const int32_t* btr = a.bt + (int64_t)seq * a.max_blocks;
   const int64_t tok_stride = (int64_t)a.kv_heads * kHeadDim;
-  const int64_t lane_off = (int64_t)r * tok_stride + (int64_t)kvh * kHeadDim + c * 8;
+  const int64_t lane_off = (int64_t)(2 * rp) * tok_stride + (int64_t)kvh * kHeadDim + 8 * dg;
   auto block_ptr = [&](int b) -> int64_t {
     int phys = btr[b];
     phys = ((uint32_t)phys < (uint64_t)a.num_blocks) ? phys : 0;  // out-of-range table entries read block 0
     return (int64_t)phys * kBlock * tok_stride + lane_off;
   };
-
-  int b = start / kBlock + wave;
-  uint4 kv[4], vv[4];
-  if (b < b1) {
+  // [row rr][half]: rows 2rp + rr, dims 8dg.. (half 0) and 64 + 8dg.. (half 1)
+  auto load_block = [&](int b, uint4 (&kr)[2][2], uint4 (&vr)[2][2]) {
     const int64_t base = block_ptr(b);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      kv[i] = *(const uint4*)(a.kc + base + 4 * i * tok_stride);
-      vv[i] = *(const uint4*)(a.vc + base + 4 * i * tok_stride);
-    }
-  }
-  for (; b < b1; b += W) {
-    uint4 kn[4], vn[4];
-    const bool more = b + W < b1;
-    if (more) {
-      const int64_t base = block_ptr(b + W);
+    for (int rr = 0; rr < 2; ++rr)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        kn[i] = *(const uint4*)(a.kc + base + 4 * i * tok_stride);
-        vn[i] = *(const uint4*)(a.vc + base + 4 * i * tok_stride);
+      for (int hf = 0; hf < 2; ++hf) {
+        kr[rr][hf] = *(const uint4*)(a.kc + base + rr * tok_stride + 64 * hf);
+        vr[rr][hf] = *(const uint4*)(a.vc + base + rr * tok_stride + 64 * hf);
       }
-    }
-    float s[G][4];
+  };
+
+  // One block of q.k, online softmax and p.v on K/V registers kr, vr (wave-uniform block index).
+  auto process = [&](int blk, const uint4 (&kr)[2][2], uint4 (&vr)[2][2]) {
+    float sc[G][2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float kf[8];
-      unpack8(kv[i], kf);
+    for (int rr = 0; rr < 2; ++rr) {
+      const uint32_t kw[8] = {kr[rr][0].x, kr[rr][0].y, kr[rr][0].z, kr[rr][0].w,
+                              kr[rr][1].x, kr[rr][1].y, kr[rr][1].z, kr[rr][1].w};
 #pragma unroll
       for (int h = 0; h < G; ++h) {
         float d = 0.f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) d = fmaf(qf[h][e], kf[e], d);
-        s[h][i] = row16_sum(d);
-      }
-      if (b * kBlock + 4 * i + r >= end) {
-#pragma unroll
-        for (int h = 0; h < G; ++h) s[h][i] = -INFINITY;
-        vv[i] = uint4{0, 0, 0, 0};  // masked rows contribute exactly zero even if stale
+        for (int e = 0; e < 8; ++e) d = dot2(kw[e], qv[h][e], d);
+        sc[h][rr] = group8_sum(d) * a.scale_log2;
       }
     }
+    if (blk * kBlock + kBlock > end) {  // the split's last, partial block
+#pragma unroll
+      for (int rr = 0; rr < 2; ++rr) {
+        if (blk * kBlock + 2 * rp + rr >= end) {
+#pragma unroll
+          for (int h = 0; h < G; ++h) sc[h][rr] = -INFINITY;
+          vr[rr][0] = uint4{0, 0, 0, 0};  // masked rows contribute exactly zero even if stale
+          vr[rr][1] = uint4{0, 0, 0, 0};
+        }
+      }
+    }
+    uint32_t pp[G];
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-      float bm = fmaxf(fmaxf(s[h][0], s[h][1]), fmaxf(s[h][2], s[h][3]));
-      bm = xrow_max(bm);  // every block holds at least one visible key
-      const float mn = fmaxf(m[h], bm);
-      const float alpha = exp2f(m[h] - mn);
-      m[h] = mn;
-      l[h] *= alpha;
+      const float bm = rowpair_max(fmaxf(sc[h][0], sc[h][1]));  // finite: row 0 of the block is visible
+      if (bm > m[h]) {  // wave-uniform
+        const float alpha = exp2f(m[h] - bm);
+        m[h] = bm;
+        l[h] *= alpha;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[h][e] *= alpha;
+        for (int e = 0; e < 16; ++e) acc[h][e] *= alpha;
+      }
+      pp[h] = pack_bf16x2(exp2f(sc[h][0] - m[h]), exp2f(sc[h][1] - m[h]));
+      l[h] += bf16lo(pp[h]) + bf16hi(pp[h]);  // the weights actually applied
+    }
+    const uint32_t v0[8] = {vr[0][0].x, vr[0][0].y, vr[0][0].z, vr[0][0].w,
+                            vr[0][1].x, vr[0][1].y, vr[0][1].z, vr[0][1].w};
+    const uint32_t v1[8] = {vr[1][0].x, vr[1][0].y, vr[1][0].z, vr[1][0].w,
+                            vr[1][1].x, vr[1][1].y, vr[1][1].z, vr[1][1].w};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        s[h][i] = exp2f(s[h][i] - mn);
-        l[h] += s[h][i];
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t lo = __builtin_amdgcn_perm(v1[e], v0[e], 0x05040100u);  // (v0[2e], v1[2e])
+      const uint32_t hi = __builtin_amdgcn_perm(v1[e], v0[e], 0x07060302u);  // (v0[2e+1], v1[2e+1])
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        acc[h][2 * e] = dot2(lo, pp[h], acc[h][2 * e]);
+        acc[h][2 * e + 1] = dot2(hi, pp[h], acc[h][2 * e + 1]);
       }
     }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float vf[8];
-      unpack8(vv[i], vf);
-#pragma unroll
-      for (int h = 0; h < G; ++h)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(s[h][i], vf[e], acc[h][e]);
-    }
-    if (more) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        kv[i] = kn[i];
-        vv[i] = vn[i];
-      }
-    }
+  };
+
+  // Two register buffers in turn: the next block's loads are in flight while one is processed.
+  int b = start / kBlock + wave;
+  uint4 ka[2][2], va[2][2], kb[2][2], vb[2][2];
+  if (b < b1) load_block(b, ka, va);
+  while (b < b1) {
+    if (b + W < b1) load_block(b + W, kb, vb);
+    process(b, ka, va);
+    b += W;
+    if (b >= b1) break;
+    if (b + W < b1) load_block(b + W, ka, va);
+    process(b, kb, vb);
+    b += W;
   }
-  // Merge the four token rows of the wavefront, then the wavefronts through LDS.
+  // Merge the row pairs of the wavefront (lanes dg, dg + 8, ...), then the wavefronts through LDS.
+  // acc[h][e]: dim 8dg + e for e < 8, 64 + 8dg + (e - 8) for e >= 8.
 #pragma unroll
   for (int h = 0; h < G; ++h) {
-    l[h] = xrow_sum(l[h]);
+    l[h] = rowpair_sum(l[h]);  // the 8 row pairs; each lane of a pair already holds the pair's sum
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[h][e] = xrow_sum(acc[h][e]);
-    if (r == 0) {
+    for (int e = 0; e < 16; ++e) acc[h][e] = rowpair_sum(acc[h][e]);
+    if (rp == 0) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) s_acc[wave][h][c * 8 + e] = acc[h][e];
+      for (int e = 0; e < 8; ++e) {
+        s_acc[wave][h][8 * dg + e] = acc[h][e];
+        s_acc[wave][h][64 + 8 * dg + e] = acc[h][8 + e];
+      }
     }
     if (lane == 0) {
       s_ml[wave][h][0] = m[h];  // -inf for a wavefront that got no block
@@ -398,8 +442,10 @@ extern "C" size_t msa_paged_attention_decode_workspace_size(int num_seqs, int he
 namespace msa {
 template <int G>
 static void launch_decode(const DecodeArgs& a, int num_seqs, hipStream_t s) {
-  // Eight wavefronts per workgroup; four when eight query heads' state would not fit.
-  constexpr int W = G >= 8 ? 4 : 8;
+  // Four wavefronts per workgroup: at the kernel's register count (three or more wavefronts per
+  // SIMD for G <= 2) three workgroups share a CU, so a batch's (sequence, KV head) pairs are
+  // resident at once.
+  constexpr int W = 4;
   const dim3 grid(a.splits, num_seqs, a.kv_heads);
   hipLaunchKernelGGL((paged_decode_kernel<G, W>), grid, dim3(64 * W), 0, s, a);
 }

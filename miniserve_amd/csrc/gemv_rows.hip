@@ -1,0 +1,734 @@
+// Token-split int8 linears for decode-sized batches, with the layer's neighbouring ops fused in.
+//
+// A workgroup owns R weight rows (R = RT x NTW x 16) and one chunk of at most 16 tokens over the
+// WHOLE of K, so no output is ever split across workgroups: there are no float32 partials and no
+// reduction kernel. Parallelism comes from rows x token chunks instead of from K.
+//
+//  1. Each wavefront first issues the 16-byte loads of all its int8 weights (its row tile(s) over
+//     its K slice) into registers: the HBM round trip starts before anything else happens.
+//  2. Meanwhile the workgroup stages its tokens' activations in LDS ([16][K + 8] bf16, rows padded
+//     by 16 bytes against bank conflicts), applying the prologue on the way: optionally gathering
+//     rows by index (embedding lookup / sampled rows) and an RMSNorm (model/layers.py:18-22 rounding:
+//     bf16(w * bf16(x * rsqrt(mean(x^2) + eps)))). The activations are small and L2-resident.
+//  3. Weights are dequantized in registers to bf16(q * s) -- the value the reference's
+//     whole-matrix dequantization produces (quant/int8.py:36) -- and multiplied on
+//     v_mfma_f32_16x16x32_bf16 (tokens as the A rows, weight rows as the B columns), accumulating
+//     in float32; when a row tile's K is split over KW wavefronts they meet in LDS.
+//  4. Epilogue on the finished tile: plain bf16 store; residual add (model/qwen3.py:121-122);
+//     silu(gate) * up with gate and up rows in the same wavefront (model/layers.py:77-78); or, for
+//     the qkv projection with one head per workgroup, the per-head q/k RMSNorm, RoPE and the
+//     K/V-cache write of model/qwen3.py:94-98 + attention/backends.py:159-160.
+//
+// Block -> (row block, token chunk) is XCD-aware: the token chunks of one row block land on one
+// XCD (workgroups go round-robin over the 8 XCDs), so its weight rows come from HBM once and the
+// other chunks hit that XCD's L2.
+//
+// The bf16 LM head with greedy argmax (model/qwen3.py:155-158 + runner/sampler.py:59) uses the
+// same structure with bf16 weights and writes one (max, first index) candidate per row block and
+// token; a second small kernel picks each token's winner.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "common.h"
+
+namespace msa {
+
+constexpr int kRowsChunk = 64;  // K per int8 chunk: one 16-byte load per lane per row tile
+constexpr int kTileTok = 16;    // token rows of the LDS activation tile (the MFMA A rows)
+
+enum { RB_PRO_NONE = 0, RB_PRO_RMSNORM = 1, RB_PRO_GATHER_RMSNORM = 2, RB_PRO_GATHER = 3 };
+enum { RB_EPI_NONE = 0, RB_EPI_SILU_MUL = 1, RB_EPI_RESIDUAL = 2, RB_EPI_QKV = 3, RB_EPI_ARGMAX = 4 };
+
+struct RowsArgs {
+  // activations (prologue)
+  const uint16_t* x;
+  int64_t ldx;
+  int64_t x_rows;         // rows of x (gathered indices are clamped into range)
+  const int64_t* gather;  // RB_PRO_GATHER*: activation row of each token
+  const uint16_t* norm_w;
+  float eps;
+  uint16_t* x_copy;  // optional: rows as gathered (before the norm) are also written here
+  int64_t ld_copy;
+  int t;    // tokens
+  int k;    // in features
+  int tpw;  // tokens per workgroup (8 or 16)
+  // weights
+  const void* w;  // int8 [n, k] (or bf16 for the LM head)
+  const uint16_t* scale;
+  int n;
+  int n_rb;  // row blocks
+  int n_mc;  // token chunks
+  // outputs
+  uint16_t* y;
+  int64_t ldy;
+  const uint16_t* resid;
+  int64_t ldr;
+  // qkv head epilogue
+  int heads;
+  int kv_heads;
+  const uint16_t* qn_w;
+  const uint16_t* kn_w;
+  float head_eps;
+  const int64_t* positions;
+  const float* cos_t;  // [max_pos, 128] float32
+  const float* sin_t;
+  int64_t max_pos;
+  const int64_t* slots;
+  uint16_t* q_out;  // [t, heads, 128]
+  uint16_t* kc;     // [num_slots, kv_heads, 128]
+  uint16_t* vc;
+  int64_t num_slots;
+  // argmax candidates [t][n_rb]
+  float* cand_val;
+  int32_t* cand_idx;
+};
+
+__device__ __forceinline__ bf16x8 dequant8_rows(uint32_t lo, uint32_t hi, float s) {
+  bf16x8 r;
+  r[0] = (__bf16)((float)(signed char)(lo) * s);
+  r[1] = (__bf16)((float)(signed char)(lo >> 8) * s);
+  r[2] = (__bf16)((float)(signed char)(lo >> 16) * s);
+  r[3] = (__bf16)((float)(signed char)(lo >> 24) * s);
+  r[4] = (__bf16)((float)(signed char)(hi) * s);
+  r[5] = (__bf16)((float)(signed char)(hi >> 8) * s);
+  r[6] = (__bf16)((float)(signed char)(hi >> 16) * s);
+  r[7] = (__bf16)((float)(signed char)(hi >> 24) * s);
+  return r;
+}
+
+__device__ __forceinline__ float silu_mul_rows(float gate_acc, float up_acc) {
+  const float g = round_bf16(gate_acc);
+  const float u = round_bf16(up_acc);
+  return round_bf16(g / (1.0f + expf(-g))) * u;
+}
+
+// Sum over aligned groups of TPT lanes (TPT = 16, 32 or 64); every lane of a group gets the total.
+template <int TPT>
+__device__ __forceinline__ float group_sum(float v) {
+  v = row16_sum(v);
+  if constexpr (TPT >= 32) v += __shfl_xor(v, 16);
+  if constexpr (TPT >= 64) v += __shfl_xor(v, 32);
+  return v;
+}
+
+// The grid holds round_up(n_rb, 8) * n_mc workgroups; rb >= n_rb marks a surplus one (it exits).
+__device__ __forceinline__ void block_to_tile(const RowsArgs& a, int& rb, int& mc) {
+  const int b = blockIdx.x;
+  const int xcd = b & 7, slot = b >> 3;
+  rb = (slot / a.n_mc) * 8 + xcd;
+  mc = slot % a.n_mc;
+}
+
+// Stage the tile's 16 activation rows in LDS (rows past the chunk repeat its last token), with the
+// prologue applied. NTH threads; TPT = NTH / 16 threads per row. Loads go out XB 16-byte vectors
+// per thread at a time and are waited for together: one memory round trip per XB vectors (for the
+// decode shapes, one in all), with the norm weights fetched alongside the first batch.
+template <int NTH, int PRO>
+__device__ __forceinline__ void stage_x(const RowsArgs& a, uint16_t* xs, int t0, int tcount, bool write_copy) {
+  constexpr int TPT = NTH / kTileTok;
+  constexpr int XB = 8;
+  constexpr bool NORM = PRO == RB_PRO_RMSNORM || PRO == RB_PRO_GATHER_RMSNORM;
+  const int ldsx = a.k + 8;
+  const int tl = threadIdx.x / TPT, q = threadIdx.x % TPT;
+  const int tok = t0 + (tl < tcount ? tl : tcount - 1);
+  int64_t src_row = tok;
+  if constexpr (PRO == RB_PRO_GATHER_RMSNORM || PRO == RB_PRO_GATHER) {
+    src_row = a.gather[tok];
+    src_row = src_row < 0 ? 0 : (src_row >= a.x_rows ? a.x_rows - 1 : src_row);  // memory safety only
+  }
+  const uint16_t* src = a.x + src_row * a.ldx;
+  uint16_t* dst = xs + tl * ldsx;
+  const int nvec = a.k / 8;
+  const bool copy = NORM && write_copy && a.x_copy != nullptr && tl < tcount;
+  uint4 nw0[NORM ? XB : 1];
+  float ss = 0.f;
+  for (int v0 = q; v0 < nvec; v0 += XB * TPT) {
+    uint4 u[XB];
+#pragma unroll
+    for (int b = 0; b < XB; ++b) {
+      const int v = v0 + b * TPT;
+      u[b] = v < nvec ? *(const uint4*)(src + v * 8) : uint4{0, 0, 0, 0};
+      if constexpr (NORM) {
+        if (v0 == q) nw0[b] = v < nvec ? *(const uint4*)(a.norm_w + v * 8) : uint4{0, 0, 0, 0};
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < XB; ++b) {
+      const int v = v0 + b * TPT;
+      if (v < nvec) {
+        *(uint4*)(dst + v * 8) = u[b];
+        if constexpr (NORM) {
+          if (copy) *(uint4*)(a.x_copy + (int64_t)tok * a.ld_copy + v * 8) = u[b];
+          const uint32_t e[4] = {u[b].x, u[b].y, u[b].z, u[b].w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float lo = bf16lo(e[i]), hi = bf16hi(e[i]);
+            ss += lo * lo + hi * hi;
+          }
+        }
+      }
+    }
+  }
+  if constexpr (NORM) {
+    ss = group_sum<TPT>(ss);
+    const float r = 1.0f / sqrtf(ss / (float)a.k + a.eps);
+    for (int v0 = q; v0 < nvec; v0 += XB * TPT) {
+      uint4 wv[XB];
+#pragma unroll
+      for (int b = 0; b < XB; ++b) {
+        const int v = v0 + b * TPT;
+        wv[b] = v0 == q ? nw0[b] : (v < nvec ? *(const uint4*)(a.norm_w + v * 8) : uint4{0, 0, 0, 0});
+      }
+#pragma unroll
+      for (int b = 0; b < XB; ++b) {
+        const int v = v0 + b * TPT;
+        if (v < nvec) {
+          const uint4 u = *(const uint4*)(dst + v * 8);  // this thread's own LDS stores above
+          const uint32_t e[4] = {u.x, u.y, u.z, u.w}, ww[4] = {wv[b].x, wv[b].y, wv[b].z, wv[b].w};
+          uint32_t o[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float lo = round_bf16(bf16lo(e[i]) * r), hi = round_bf16(bf16hi(e[i]) * r);
+            o[i] = pack_bf16x2(bf16lo(ww[i]) * lo, bf16hi(ww[i]) * hi);
+          }
+          *(uint4*)(dst + v * 8) = uint4{o[0], o[1], o[2], o[3]};
+        }
+      }
+    }
+  }
+}
+
+// Weight row of (row block rb, row tile rt, sub-tile nt, lane row j).
+template <int RT, int NTW, int EPI>
+__device__ __forceinline__ int rows_row(const RowsArgs& a, int rb, int rt, int nt, int j) {
+  if constexpr (EPI == RB_EPI_SILU_MUL) {
+    return (nt == 0 ? 0 : a.n / 2) + rb * (RT * 16) + rt * 16 + j;  // NTW == 2: [gate | up]
+  } else {
+    return rb * (RT * NTW * 16) + (rt * NTW + nt) * 16 + j;
+  }
+}
+
+// The qkv epilogue: ot holds bf16-rounded outputs [16 tokens][128 + 4] of head slot hs (q heads,
+// then k heads, then v heads). q/k: per-head RMSNorm then RoPE with pairs (i, i + 64), rounding as
+// model/layers.py:18-22 and :61-65; v: copied. Keys and values go to the cache slot of their token.
+template <int NTH>
+__device__ __forceinline__ void qkv_head_epilogue(const RowsArgs& a, const float* ot, int hs, int t0, int tcount) {
+  constexpr int D = 128, HALF = 64, OTS = D + 4;
+  constexpr int TPT = NTH / kTileTok;  // threads per token
+  constexpr int PPT = HALF / TPT;      // rotary pairs per thread
+  const int tl = threadIdx.x / TPT, q = threadIdx.x % TPT;
+  if (tl >= tcount) return;  // whole groups leave together; no barrier follows
+  const int tok = t0 + tl;
+  const float* row = ot + tl * OTS;
+  const bool is_q = hs < a.heads, is_v = hs >= a.heads + a.kv_heads;
+  uint16_t* dst;
+  if (is_q) {
+    dst = a.q_out + ((int64_t)tok * a.heads + hs) * D;
+  } else {
+    const int64_t slot = a.slots[tok];
+    if (slot < 0 || slot >= a.num_slots) return;
+    const int kvh = is_v ? hs - a.heads - a.kv_heads : hs - a.heads;
+    dst = (is_v ? a.vc : a.kc) + (slot * a.kv_heads + kvh) * D;
+  }
+  if (is_v) {
+#pragma unroll
+    for (int p = 0; p < PPT; ++p) {
+      const int i = q + p * TPT;
+      dst[i] = f32_to_bf16(row[i]);
+      dst[i + HALF] = f32_to_bf16(row[i + HALF]);
+    }
+    return;
+  }
+  float lo[PPT], hi[PPT], ss = 0.f;
+#pragma unroll
+  for (int p = 0; p < PPT; ++p) {
+    const int i = q + p * TPT;
+    lo[p] = row[i];
+    hi[p] = row[i + HALF];
+    ss += lo[p] * lo[p] + hi[p] * hi[p];
+  }
+  ss = group_sum<TPT>(ss);
+  const float r = 1.0f / sqrtf(ss / (float)D + a.head_eps);
+  const uint16_t* nw = is_q ? a.qn_w : a.kn_w;
+  int64_t pos = a.positions[tok];
+  pos = pos < 0 ? 0 : (pos >= a.max_pos ? a.max_pos - 1 : pos);  // memory safety only
+  const float* cr = a.cos_t + pos * D;
+  const float* sr = a.sin_t + pos * D;
+#pragma unroll
+  for (int p = 0; p < PPT; ++p) {
+    const int i = q + p * TPT;
+    const float x0 = round_bf16(bf16_to_f32(nw[i]) * round_bf16(lo[p] * r));
+    const float x1 = round_bf16(bf16_to_f32(nw[i + HALF]) * round_bf16(hi[p] * r));
+    const float c0 = round_bf16(cr[i]), c1 = round_bf16(cr[i + HALF]);
+    const float s0 = round_bf16(sr[i]), s1 = round_bf16(sr[i + HALF]);
+    dst[i] = f32_to_bf16(round_bf16(x0 * c0) + round_bf16(-x1 * s0));
+    dst[i + HALF] = f32_to_bf16(round_bf16(x1 * c1) + round_bf16(x0 * s1));
+  }
+}
+
+// int8 weights. RT row tiles (x NTW sub-tiles of 16 rows) per workgroup, each row tile's K split
+// over KW wavefronts; CPW = 64-wide K chunks a wavefront holds in registers at once.
+template <int RT, int NTW, int KW, int CPW, int PRO, int EPI>
+__global__ __launch_bounds__(64 * RT * KW) void int8_rows_kernel(RowsArgs a) {
+  constexpr int NTH = 64 * RT * KW;
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  uint16_t* xs = smem;  // [16][k + 8]
+  const int ldsx = a.k + 8;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  const int rt = wave % RT, ks = wave / RT;
+  int rb, mc;
+  block_to_tile(a, rb, mc);
+  if (rb >= a.n_rb) return;  // surplus workgroup of the XCD-rounded grid (before any barrier)
+  const int t0 = mc * a.tpw;
+  const int tcount = min(a.tpw, a.t - t0);
+
+  const int8_t* wp[NTW];
+  float sc[NTW];
+#pragma unroll
+  for (int nt = 0; nt < NTW; ++nt) {
+    int row = rows_row<RT, NTW, EPI>(a, rb, rt, nt, j);
+    row = row < a.n ? row : a.n - 1;  // rows past n load row n-1; their outputs are dropped
+    wp[nt] = (const int8_t*)a.w + (int64_t)row * a.k + g * 16;
+    sc[nt] = bf16_to_f32(a.scale[row]);
+  }
+  const int nch = a.k / kRowsChunk;
+  const int per = (nch + KW - 1) / KW;
+  const int c_begin = ks * per, c_end = min(nch, c_begin + per);
+
+  uint4 wv[CPW][NTW];
+  auto load_batch = [&](int c0) {
+#pragma unroll
+    for (int c = 0; c < CPW; ++c)
+#pragma unroll
+      for (int nt = 0; nt < NTW; ++nt)
+        wv[c][nt] = c0 + c < c_end ? *(const uint4*)(wp[nt] + (int64_t)(c0 + c) * kRowsChunk) : uint4{0, 0, 0, 0};
+  };
+  load_batch(c_begin);
+  stage_x<NTH, PRO>(a, xs, t0, tcount, rb == 0);
+  __syncthreads();
+
+  f32x4 acc[NTW];
+#pragma unroll
+  for (int nt = 0; nt < NTW; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const uint16_t* xrow = xs + j * ldsx + g * 16;
+  for (int c0 = c_begin; c0 < c_end; c0 += CPW) {
+    if (c0 != c_begin) load_batch(c0);
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+      if (c0 + c < c_end) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const bf16x8 av = *(const bf16x8*)(xrow + (c0 + c) * kRowsChunk + h * 8);
+#pragma unroll
+          for (int nt = 0; nt < NTW; ++nt) {
+            const bf16x8 bv = h == 0 ? dequant8_rows(wv[c][nt].x, wv[c][nt].y, sc[nt])
+                                     : dequant8_rows(wv[c][nt].z, wv[c][nt].w, sc[nt]);
+            acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, acc[nt], 0, 0, 0);
+          }
+        }
+      }
+    }
+  }
+
+  if constexpr (KW > 1) {
+    f32x4* red = (f32x4*)(smem + kTileTok * ldsx);  // [KW - 1][RT][NTW][64]
+    if (ks > 0) {
+#pragma unroll
+      for (int nt = 0; nt < NTW; ++nt) red[(((ks - 1) * RT + rt) * NTW + nt) * 64 + lane] = acc[nt];
+    }
+    __syncthreads();
+    if (ks == 0) {
+      for (int s = 1; s < KW; ++s)
+#pragma unroll
+        for (int nt = 0; nt < NTW; ++nt) acc[nt] += red[(((s - 1) * RT + rt) * NTW + nt) * 64 + lane];
+    }
+  }
+
+  if constexpr (EPI == RB_EPI_QKV) {
+    float* ot = (float*)(smem + kTileTok * ldsx) + (KW > 1 ? (KW - 1) * RT * NTW * 256 : 0);  // [16][132]
+    if (ks == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ot[(4 * g + i) * 132 + rt * 16 + j] = round_bf16(acc[0][i]);
+    }
+    __syncthreads();
+    qkv_head_epilogue<NTH>(a, ot, rb, t0, tcount);
+    return;
+  } else {
+    if (ks != 0) return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int tl = 4 * g + i;
+      if (tl >= tcount) continue;
+      const int64_t tok = t0 + tl;
+      if constexpr (EPI == RB_EPI_SILU_MUL) {
+        const int col = rb * (RT * 16) + rt * 16 + j;
+        if (col < a.n / 2) a.y[tok * a.ldy + col] = f32_to_bf16(silu_mul_rows(acc[0][i], acc[1][i]));
+      } else {
+#pragma unroll
+        for (int nt = 0; nt < NTW; ++nt) {
+          const int row = rows_row<RT, NTW, EPI>(a, rb, rt, nt, j);
+          if (row >= a.n) continue;
+          float v = round_bf16(acc[nt][i]);
+          if constexpr (EPI == RB_EPI_RESIDUAL) v += bf16_to_f32(a.resid[tok * a.ldr + row]);
+          a.y[tok * a.ldy + row] = f32_to_bf16(v);
+        }
+      }
+    }
+  }
+}
+
+// bf16 LM head + greedy argmax, persistent over vocabulary row tiles. A workgroup (W waves)
+// stages up to 64 sampled rows, normalized once, in LDS ([64][K + 8] bf16), then its waves take
+// 16-row tiles of the weight round-robin (tiles wg * W + wave, + W * gridDim, ...). Per tile a
+// lane streams its row's K in 32-wide chunks (one 16-byte bf16 load per chunk, PF chunks in
+// flight), multiplies on MFMA against the MT token tiles, rounds each logit to bf16 (the
+// reference's logits dtype) and keeps a running (max, first index) per token. The waves then meet
+// in LDS and write one candidate per (workgroup, token); argmax_candidates_kernel picks the winner.
+template <int W, int MT, int PRO>
+__global__ __launch_bounds__(64 * W) void lm_head_argmax_kernel(RowsArgs a) {
+  constexpr int CH = 32;  // K per chunk (bf16: 16 bytes per lane)
+  constexpr int PF = 8;   // chunks in flight per wave
+  constexpr int NTH = 64 * W;
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  const int ldsx = a.k + 8;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 15, g = lane >> 4;
+
+  // Stage the (up to 64) rows: 16-row tiles, each with the RMSNorm prologue.
+  for (int mt = 0; mt < MT; ++mt) {
+    const int t0 = mt * 16;
+    const int tcount = max(1, min(16, a.t - t0));
+    stage_x<NTH, PRO>(a, smem + mt * 16 * ldsx, min(t0, a.t - 1), tcount, false);
+  }
+  __syncthreads();
+
+  float best[MT][4];
+  int bidx[MT][4];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      best[mt][i] = -INFINITY;
+      bidx[mt][i] = 0x7fffffff;
+    }
+  const int ntiles = (a.n + 15) / 16;
+  const int nch = a.k / CH;
+  for (int tile = blockIdx.x * W + wave; tile < ntiles; tile += gridDim.x * W) {
+    const int row = tile * 16 + j;
+    const uint16_t* wp = (const uint16_t*)a.w + (int64_t)(row < a.n ? row : a.n - 1) * a.k + g * 8;
+    f32x4 acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    uint4 wv[PF];
+#pragma unroll
+    for (int c = 0; c < PF; ++c) wv[c] = c < nch ? *(const uint4*)(wp + c * CH) : uint4{0, 0, 0, 0};
+    for (int c0 = 0; c0 < nch; c0 += PF) {
+#pragma unroll
+      for (int c = 0; c < PF; ++c) {
+        if (c0 + c < nch) {
+          const uint4 cur = wv[c];
+          if (c0 + c + PF < nch) wv[c] = *(const uint4*)(wp + (c0 + c + PF) * CH);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            const bf16x8 av = *(const bf16x8*)(smem + (mt * 16 + j) * ldsx + (c0 + c) * CH + g * 8);
+            acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8, cur), acc[mt], 0, 0, 0);
+          }
+        }
+      }
+    }
+    // lane (g, j) holds logits of tokens mt*16 + 4g + i for vocabulary row `row`
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float v = row < a.n ? round_bf16(acc[mt][i]) : -INFINITY;
+        if (v > best[mt][i]) {  // rows arrive in increasing order per lane: ties keep the first
+          best[mt][i] = v;
+          bidx[mt][i] = row;
+        }
+      }
+  }
+  // Reduce over the 16 lanes j (rows), then over the waves through LDS.
+  float* cv = (float*)(smem + MT * 16 * ldsx);  // [W][64]
+  int32_t* ci = (int32_t*)(cv + W * 64);        // [W][64]
+  __syncthreads();  // every wave is done reading the activation tile? (cv lies past it; kept for order)
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float v = best[mt][i];
+      int idx = bidx[mt][i];
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) {
+        const float ov = __shfl_xor(v, off);
+        const int oi = __shfl_xor(idx, off);
+        if (ov > v || (ov == v && oi < idx)) {
+          v = ov;
+          idx = oi;
+        }
+      }
+      if (j == 0) {
+        cv[wave * 64 + mt * 16 + 4 * g + i] = v;
+        ci[wave * 64 + mt * 16 + 4 * g + i] = idx;
+      }
+    }
+  __syncthreads();
+  if (threadIdx.x < 64 && (int)threadIdx.x < a.t) {
+    const int t = threadIdx.x;
+    float v = cv[t];
+    int idx = ci[t];
+    for (int w = 1; w < W; ++w) {
+      const float ov = cv[w * 64 + t];
+      const int oi = ci[w * 64 + t];
+      if (ov > v || (ov == v && oi < idx)) {
+        v = ov;
+        idx = oi;
+      }
+    }
+    a.cand_val[(int64_t)t * gridDim.x + blockIdx.x] = v;
+    a.cand_idx[(int64_t)t * gridDim.x + blockIdx.x] = idx;
+  }
+}
+
+// One workgroup per token: the maximum over its row blocks' candidates, first index on ties.
+__global__ __launch_bounds__(256) void argmax_candidates_kernel(const float* __restrict__ cv, const int32_t* __restrict__ ci,
+                                                                int n_rb, int64_t* __restrict__ out) {
+  __shared__ float sv[4];
+  __shared__ int si[4];
+  const int tok = blockIdx.x;
+  float v = -INFINITY;
+  int idx = 0x7fffffff;
+  for (int r = threadIdx.x; r < n_rb; r += 256) {
+    const float ov = cv[(int64_t)tok * n_rb + r];
+    const int oi = ci[(int64_t)tok * n_rb + r];
+    if (ov > v || (ov == v && oi < idx)) {
+      v = ov;
+      idx = oi;
+    }
+  }
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const float ov = __shfl_xor(v, off);
+    const int oi = __shfl_xor(idx, off);
+    if (ov > v || (ov == v && oi < idx)) {
+      v = ov;
+      idx = oi;
+    }
+  }
+  if ((threadIdx.x & 63) == 0) {
+    sv[threadIdx.x >> 6] = v;
+    si[threadIdx.x >> 6] = idx;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 4; ++w) {
+      if (sv[w] > v || (sv[w] == v && si[w] < idx)) {
+        v = sv[w];
+        idx = si[w];
+      }
+    }
+    out[tok] = idx;
+  }
+}
+
+// ---- host side ----------------------------------------------------------------------------------
+
+template <typename K>
+static int launch_rows(K kernel, int nth, size_t lds, int blocks, const RowsArgs& a, hipStream_t s) {
+  if (lds > 64 * 1024) {
+    hipError_t e = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return fail(MSA_ERR_LAUNCH, std::string("hipFuncSetAttribute: ") + hipGetErrorString(e));
+  }
+  hipLaunchKernelGGL(kernel, dim3(blocks), dim3(nth), lds, s, a);
+  return MSA_OK;
+}
+
+static size_t x_tile_bytes(int k) { return (size_t)kTileTok * (k + 8) * 2; }
+static int grid_blocks(const RowsArgs& a) { return ((a.n_rb + 7) / 8) * 8 * a.n_mc; }
+constexpr size_t kMaxLds = 160 * 1024;
+
+static int tokens_per_wg(int64_t, int) {
+  // Full 16-token chunks: every chunk repeats the dequantization of the row block's weights (the
+  // kernels are bound by VALU issue), so smaller chunks cost more than the CUs they would fill.
+  return 16;
+}
+
+}  // namespace msa
+
+using namespace msa;
+
+// Shapes handled by the token-split kernels: k % 64 == 0, the activation tile fits in LDS.
+extern "C" int msa_int8_linear_rows(const uint16_t* x, int64_t ldx, int64_t m, int64_t k, const uint16_t* norm_w,
+                                    float eps, const int8_t* qweight, const uint16_t* scale, int64_t n, int epilogue,
+                                    uint16_t* y, int64_t ldy, const uint16_t* residual, int64_t ldr,
+                                    msa_stream_t stream) {
+  if (m == 0) return MSA_OK;
+  if (!x || !qweight || !scale || !y) return fail(MSA_ERR_INVALID, "msa_int8_linear_rows: null pointer");
+  if (m < 0 || n <= 0 || k <= 0 || m > 0x7fffffff || n > 0x7fffffff)
+    return fail(MSA_ERR_INVALID, "msa_int8_linear_rows: bad shape");
+  if (k % 64 != 0) return fail(MSA_ERR_UNSUPPORTED, "msa_int8_linear_rows: in_features must be a multiple of 64");
+  if (x_tile_bytes((int)k) + 16 * 1024 > kMaxLds)
+    return fail(MSA_ERR_UNSUPPORTED, "msa_int8_linear_rows: in_features too large for the LDS activation tile");
+  if (ldx < k || ldx % 8 != 0 || !aligned16(x) || !aligned16(qweight))
+    return fail(MSA_ERR_INVALID, "msa_int8_linear_rows: x / qweight must be 16-byte aligned with ldx % 8 == 0");
+  if (norm_w && !aligned16(norm_w)) return fail(MSA_ERR_INVALID, "msa_int8_linear_rows: norm_w must be 16-byte aligned");
+  if (norm_w && epilogue != MSA_EPI_SILU_MUL)
+    return fail(MSA_ERR_UNSUPPORTED, "msa_int8_linear_rows: the RMSNorm prologue is fused with MSA_EPI_SILU_MUL only");
+  if (epilogue == MSA_EPI_SILU_MUL && n % 2 != 0) return fail(MSA_ERR_INVALID, "msa_int8_linear_rows: SILU_MUL needs an even n");
+  const int64_t out_cols = epilogue == MSA_EPI_SILU_MUL ? n / 2 : n;
+  if (ldy < out_cols) return fail(MSA_ERR_INVALID, "msa_int8_linear_rows: ldy too small");
+  if (epilogue == MSA_EPI_RESIDUAL && (!residual || ldr < n))
+    return fail(MSA_ERR_INVALID, "msa_int8_linear_rows: the residual epilogue needs residual with ldr >= n");
+  const int pro = norm_w ? RB_PRO_RMSNORM : RB_PRO_NONE;
+
+  RowsArgs a{};
+  a.x = x; a.ldx = ldx; a.x_rows = m; a.norm_w = norm_w; a.eps = eps;
+  a.t = (int)m; a.k = (int)k; a.w = qweight; a.scale = scale; a.n = (int)n;
+  a.y = y; a.ldy = ldy; a.resid = residual; a.ldr = ldr;
+  hipStream_t s = (hipStream_t)stream;
+  const size_t xt = x_tile_bytes((int)k);
+  int rc;
+  if (epilogue == MSA_EPI_SILU_MUL) {
+    // 64 gate + 64 up rows per workgroup: 4 row tiles x (gate, up) x 2 K slices.
+    a.n_rb = (int)((n / 2 + 63) / 64);
+    a.tpw = tokens_per_wg(m, a.n_rb);
+    a.n_mc = (int)((m + a.tpw - 1) / a.tpw);
+    const size_t lds = xt + 1 * 4 * 2 * 1024;
+    if (pro == RB_PRO_RMSNORM)
+      rc = launch_rows(int8_rows_kernel<4, 2, 2, 8, RB_PRO_RMSNORM, RB_EPI_SILU_MUL>, 512, lds, grid_blocks(a), a, s);
+    else
+      rc = launch_rows(int8_rows_kernel<4, 2, 2, 8, RB_PRO_NONE, RB_EPI_SILU_MUL>, 512, lds, grid_blocks(a), a, s);
+  } else if (epilogue == MSA_EPI_RESIDUAL || epilogue == MSA_EPI_NONE) {
+    // 16 rows per workgroup, K over 8 wavefronts: narrow outputs (o_proj / down_proj) still give
+    // rows/16 x token-chunks workgroups.
+    a.n_rb = (int)((n + 15) / 16);
+    a.tpw = tokens_per_wg(m, a.n_rb);
+    a.n_mc = (int)((m + a.tpw - 1) / a.tpw);
+    const size_t lds = xt + 7 * 1 * 1 * 1024;
+    if (epilogue == MSA_EPI_RESIDUAL)
+      rc = launch_rows(int8_rows_kernel<1, 1, 8, 8, RB_PRO_NONE, RB_EPI_RESIDUAL>, 512, lds, grid_blocks(a), a, s);
+    else
+      rc = launch_rows(int8_rows_kernel<1, 1, 8, 8, RB_PRO_NONE, RB_EPI_NONE>, 512, lds, grid_blocks(a), a, s);
+  } else {
+    return fail(MSA_ERR_INVALID, "msa_int8_linear_rows: unknown epilogue");
+  }
+  if (rc != MSA_OK) return rc;
+  return check_launch("msa_int8_linear_rows");
+}
+
+extern "C" int msa_qkv_rope_cache_rows(const uint16_t* x, int64_t ldx, int64_t x_rows, const int64_t* gather_rows,
+                                       const uint16_t* norm_w, float eps, uint16_t* x_copy, int64_t ld_copy,
+                                       int64_t tokens, int64_t hidden, const int8_t* qweight, const uint16_t* scale,
+                                       int heads, int kv_heads, int head_dim, const uint16_t* q_norm_w,
+                                       const uint16_t* k_norm_w, float qk_eps, const int64_t* positions,
+                                       const float* cos_table, const float* sin_table, int64_t max_positions,
+                                       const int64_t* slot_mapping, uint16_t* q_out, uint16_t* k_cache,
+                                       uint16_t* v_cache, int64_t num_slots, msa_stream_t stream) {
+  if (tokens == 0) return MSA_OK;
+  if (!x || !qweight || !scale || !q_norm_w || !k_norm_w || !positions || !cos_table || !sin_table || !slot_mapping ||
+      !q_out || !k_cache || !v_cache)
+    return fail(MSA_ERR_INVALID, "msa_qkv_rope_cache_rows: null pointer");
+  if (head_dim != 128) return fail(MSA_ERR_UNSUPPORTED, "msa_qkv_rope_cache_rows: head_dim must be 128");
+  if (tokens < 0 || tokens > 0x7fffffff || heads <= 0 || kv_heads <= 0 || heads % kv_heads != 0 || max_positions <= 0)
+    return fail(MSA_ERR_INVALID, "msa_qkv_rope_cache_rows: bad shape");
+  if (hidden <= 0 || hidden % 64 != 0) return fail(MSA_ERR_UNSUPPORTED, "msa_qkv_rope_cache_rows: hidden must be a multiple of 64");
+  const size_t lds = x_tile_bytes((int)hidden) + 16 * 132 * 4;  // x tile, head tile
+  if (lds > kMaxLds) return fail(MSA_ERR_UNSUPPORTED, "msa_qkv_rope_cache_rows: hidden too large for the LDS activation tile");
+  if (ldx < hidden || ldx % 8 != 0 || !aligned16(x) || !aligned16(qweight))
+    return fail(MSA_ERR_INVALID, "msa_qkv_rope_cache_rows: x / qweight must be 16-byte aligned with ldx % 8 == 0");
+  if (x_rows < (gather_rows ? 1 : tokens)) return fail(MSA_ERR_INVALID, "msa_qkv_rope_cache_rows: x has too few rows");
+  if (gather_rows && !norm_w) return fail(MSA_ERR_UNSUPPORTED, "msa_qkv_rope_cache_rows: gather_rows needs norm_w");
+  if (norm_w && !aligned16(norm_w)) return fail(MSA_ERR_INVALID, "msa_qkv_rope_cache_rows: norm_w must be 16-byte aligned");
+  if (x_copy && (!aligned16(x_copy) || ld_copy < hidden || ld_copy % 8 != 0))
+    return fail(MSA_ERR_INVALID, "msa_qkv_rope_cache_rows: x_copy must be 16-byte aligned with ld_copy >= hidden");
+  const int pro = gather_rows ? RB_PRO_GATHER_RMSNORM : (norm_w ? RB_PRO_RMSNORM : RB_PRO_NONE);
+  RowsArgs a{};
+  a.x = x; a.ldx = ldx; a.x_rows = x_rows; a.gather = gather_rows; a.norm_w = norm_w; a.eps = eps;
+  a.x_copy = x_copy; a.ld_copy = ld_copy;
+  a.t = (int)tokens; a.k = (int)hidden; a.w = qweight; a.scale = scale; a.n = (heads + 2 * kv_heads) * 128;
+  a.heads = heads; a.kv_heads = kv_heads; a.qn_w = q_norm_w; a.kn_w = k_norm_w;
+  a.positions = positions; a.cos_t = cos_table; a.sin_t = sin_table; a.max_pos = max_positions;
+  a.slots = slot_mapping; a.q_out = q_out; a.kc = k_cache; a.vc = v_cache; a.num_slots = num_slots;
+  a.head_eps = qk_eps;
+  a.n_rb = heads + 2 * kv_heads;  // one head (128 weight rows) per row block
+  a.tpw = tokens_per_wg(tokens, a.n_rb);
+  a.n_mc = (int)((tokens + a.tpw - 1) / a.tpw);
+  hipStream_t s = (hipStream_t)stream;
+  // 8 row tiles (one head) x the whole of K per wavefront = 8 wavefronts.
+  int rc;
+  switch (pro) {
+    case RB_PRO_NONE:
+      rc = launch_rows(int8_rows_kernel<8, 1, 1, 16, RB_PRO_NONE, RB_EPI_QKV>, 512, lds, grid_blocks(a), a, s);
+      break;
+    case RB_PRO_RMSNORM:
+      rc = launch_rows(int8_rows_kernel<8, 1, 1, 16, RB_PRO_RMSNORM, RB_EPI_QKV>, 512, lds, grid_blocks(a), a, s);
+      break;
+    default:
+      rc = launch_rows(int8_rows_kernel<8, 1, 1, 16, RB_PRO_GATHER_RMSNORM, RB_EPI_QKV>, 512, lds, grid_blocks(a), a, s);
+      break;
+  }
+  if (rc != MSA_OK) return rc;
+  return check_launch("msa_qkv_rope_cache_rows");
+}
+
+constexpr int kLmBlocks = 256;  // persistent workgroups of the LM head (one per CU)
+constexpr int kLmMaxRows = 64;  // sampled rows per launch (four 16-token MFMA tiles)
+
+extern "C" size_t msa_lm_head_argmax_workspace_size(int64_t num_rows, int64_t vocab) {
+  if (num_rows <= 0 || vocab <= 0) return 0;
+  return (size_t)num_rows * kLmBlocks * (sizeof(float) + sizeof(int32_t));
+}
+
+extern "C" int msa_lm_head_argmax(const uint16_t* hidden, int64_t ld_hidden, int64_t hidden_rows, const int64_t* rows,
+                                  int64_t num_rows, int64_t k, const uint16_t* norm_w, float eps,
+                                  const uint16_t* weight, int64_t vocab, int64_t* out_ids, void* workspace,
+                                  size_t workspace_bytes, msa_stream_t stream) {
+  if (num_rows == 0) return MSA_OK;
+  if (!hidden || !rows || !weight || !out_ids) return fail(MSA_ERR_INVALID, "msa_lm_head_argmax: null pointer");
+  if (num_rows < 0 || num_rows > 0x7fffffff || vocab <= 0 || vocab > 0x7fffffff || k <= 0 || hidden_rows <= 0)
+    return fail(MSA_ERR_INVALID, "msa_lm_head_argmax: bad shape");
+  if (k % 32 != 0) return fail(MSA_ERR_UNSUPPORTED, "msa_lm_head_argmax: hidden must be a multiple of 32");
+  if (ld_hidden < k || ld_hidden % 8 != 0 || !aligned16(hidden) || !aligned16(weight) || (norm_w && !aligned16(norm_w)))
+    return fail(MSA_ERR_INVALID, "msa_lm_head_argmax: hidden / weight / norm_w must be 16-byte aligned");
+  const size_t need = msa_lm_head_argmax_workspace_size(num_rows, vocab);
+  if (!workspace || workspace_bytes < need) return fail(MSA_ERR_WORKSPACE, "msa_lm_head_argmax: workspace too small");
+  if (!aligned16(workspace)) return fail(MSA_ERR_INVALID, "msa_lm_head_argmax: workspace must be 16-byte aligned");
+  hipStream_t s = (hipStream_t)stream;
+  float* cand_val = (float*)workspace;
+  int32_t* cand_idx = (int32_t*)((char*)workspace + (size_t)num_rows * kLmBlocks * sizeof(float));
+  // Launches of up to 64 rows each (fewer when 16-row activation tiles of this width fill LDS);
+  // every launch writes its rows' candidates. Each launch streams the whole weight once.
+  constexpr int W = 8;
+  const size_t tile_bytes = (size_t)16 * (k + 8) * 2;
+  const int64_t max_mt = std::min<int64_t>(kLmMaxRows / 16, (int64_t)((kMaxLds - 2 * W * 64 * 4) / tile_bytes));
+  if (max_mt < 1) return fail(MSA_ERR_UNSUPPORTED, "msa_lm_head_argmax: hidden too large for the LDS activation tile");
+  for (int64_t r0 = 0; r0 < num_rows; r0 += 16 * max_mt) {
+    const int nr = (int)std::min<int64_t>(16 * max_mt, num_rows - r0);
+    const int mt = (nr + 15) / 16;
+    const size_t lds = (size_t)mt * tile_bytes + 2 * W * 64 * 4;
+    RowsArgs a{};
+    a.x = hidden; a.ldx = ld_hidden; a.x_rows = hidden_rows; a.gather = rows + r0; a.norm_w = norm_w; a.eps = eps;
+    a.t = nr; a.k = (int)k; a.w = weight; a.n = (int)vocab;
+    a.cand_val = cand_val + r0 * kLmBlocks;
+    a.cand_idx = cand_idx + r0 * kLmBlocks;
+    int rc;
+#define MSA_LM_LAUNCH(MT)                                                                                        \
+  rc = norm_w ? launch_rows(lm_head_argmax_kernel<W, MT, RB_PRO_GATHER_RMSNORM>, 64 * W, lds, kLmBlocks, a, s) \
+              : launch_rows(lm_head_argmax_kernel<W, MT, RB_PRO_GATHER>, 64 * W, lds, kLmBlocks, a, s)
+    switch (mt) {
+      case 1: MSA_LM_LAUNCH(1); break;
+      case 2: MSA_LM_LAUNCH(2); break;
+      case 3: MSA_LM_LAUNCH(3); break;
+      default: MSA_LM_LAUNCH(4); break;
+    }
+#undef MSA_LM_LAUNCH
+    if (rc != MSA_OK) return rc;
+    rc = check_launch("msa_lm_head_argmax");
+    if (rc != MSA_OK) return rc;
+  }
+  hipLaunchKernelGGL(argmax_candidates_kernel, dim3((unsigned)num_rows), dim3(256), 0, s, cand_val, cand_idx,
+                     kLmBlocks, out_ids);
+  return check_launch("msa_lm_head_argmax (candidates)");
+}

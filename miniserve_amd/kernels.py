@@ -280,11 +280,11 @@ def reshape_and_cache(k: Tensor, v: Tensor, k_cache: Tensor, v_cache: Tensor, sl
 
 
 def decode_splits(num_seqs: int, kv_heads: int, max_blocks: int) -> tuple[int, int]:
-    """(partition_tokens, partitions) for the decode kernel: one workgroup of eight wavefronts per
+    """(partition_tokens, partitions) for the decode kernel: one workgroup of four wavefronts per
     (sequence, KV head) when that gives 256+ workgroups; otherwise split each sequence's keys
-    across workgroups (at least eight 16-token blocks, one per wavefront, in each)."""
+    across workgroups (at least four 16-token blocks, one per wavefront, in each)."""
     wgs = max(1, num_seqs * kv_heads)
-    splits = 1 if wgs >= 256 else min(-(-512 // wgs), max(1, max_blocks // 8))
+    splits = 1 if wgs >= 256 else min(-(-512 // wgs), max(1, max_blocks // 4))
     per_blocks = -(-max_blocks // splits)
     return per_blocks * 16, -(-max_blocks // per_blocks)
 
@@ -342,5 +342,132 @@ def paged_attention_prefill(
         "msa_paged_attention_prefill", _ptr(q), q.stride(0), _ptr(k_cache), _ptr(v_cache), k_cache.shape[0], heads,
         kvh, d, block_size, _ptr(block_tables), block_tables.shape[1], _ptr(seq_info), _ptr(work), work.shape[0],
         float(scale), _ptr(out), out.stride(0), _stream(q),
+    )
+    return out
+
+
+# ---- token-split int8 linears with fused prologues / epilogues ------------------------------------
+
+ROWS_MAX_TOKENS = 256  # above this the split-K kernels (or a prefill GEMM) serve the shape
+
+
+def rows_supported(k: int) -> bool:
+    """Whether msa_int8_linear_rows / msa_qkv_rope_cache_rows take this in_features (the [16, k]
+    activation tile has to fit in LDS next to the kernel's other scratch)."""
+    return k % 64 == 0 and 16 * (k + 8) * 2 + 16 * 1024 <= 160 * 1024
+
+
+def int8_linear_rows(
+    x: Tensor,
+    qweight: Tensor,
+    scale: Tensor,
+    epilogue: int = EPI_NONE,
+    residual: Tensor | None = None,
+    out: Tensor | None = None,
+    norm_w: Tensor | None = None,
+    eps: float = 0.0,
+) -> Tensor:
+    """y = [RMSNorm](x) @ bf16(qweight * scale)^T with the epilogue fused (token-split kernel).
+
+    x [m, k] bf16. ``norm_w`` applies RMSNorm(x) (model/layers.py:18-22) before the product
+    (SILU_MUL only). EPI_RESIDUAL returns residual + y and may write in place (out=residual).
+    """
+    _on_gpu(x, qweight, scale)
+    _check(x.dtype == torch.bfloat16 and x.dim() == 2 and x.stride(-1) == 1, "int8_linear_rows: x [m, k] bf16")
+    _check(qweight.dtype == torch.int8 and qweight.is_contiguous(), "int8_linear_rows: bad qweight")
+    n, k = qweight.shape
+    m = x.shape[0]
+    _check(x.shape[1] == k, "int8_linear_rows: x / weight feature mismatch")
+    cols = n // 2 if epilogue == EPI_SILU_MUL else n
+    if out is None:
+        out = torch.empty(m, cols, dtype=torch.bfloat16, device=x.device)
+    _check(out.shape == (m, cols) and out.stride(-1) == 1, "int8_linear_rows: bad out")
+    r2 = None
+    if epilogue == EPI_RESIDUAL:
+        _check(residual is not None and residual.shape == (m, n) and residual.stride(-1) == 1, "int8_linear_rows: residual")
+        r2 = residual
+    if norm_w is not None:
+        _check(norm_w.dtype == torch.bfloat16 and norm_w.numel() == k, "int8_linear_rows: norm weight")
+    _native.call(
+        "msa_int8_linear_rows", _ptr(x), x.stride(0), m, k, _ptr(norm_w), float(eps), _ptr(qweight), _ptr(scale), n,
+        epilogue, _ptr(out), out.stride(0), _ptr(r2), r2.stride(0) if r2 is not None else 0, _stream(x),
+    )
+    return out
+
+
+def qkv_rope_cache_rows(
+    x: Tensor,
+    qweight: Tensor,
+    scale: Tensor,
+    heads: int,
+    kv_heads: int,
+    head_dim: int,
+    q_norm_w: Tensor,
+    k_norm_w: Tensor,
+    qk_eps: float,
+    positions: Tensor,
+    cos_table: Tensor,
+    sin_table: Tensor,
+    slot_mapping: Tensor,
+    k_cache: Tensor,
+    v_cache: Tensor,
+    norm_w: Tensor | None = None,
+    eps: float = 0.0,
+    gather: Tensor | None = None,
+    x_copy: Tensor | None = None,
+) -> Tensor:
+    """The attention block's front half in one kernel: [gather rows] -> [RMSNorm] -> int8 qkv
+    projection -> per-head q/k RMSNorm -> RoPE -> k/v written at slot_mapping; returns q [T, H, D].
+
+    With ``gather`` (int64 [T]) the activation rows are x[gather] (the embedding lookup) and are
+    also written to ``x_copy`` [T, k] (the residual stream) when given. cos/sin tables are the
+    rotary's float32 [max_positions, D] tables, indexed by ``positions`` inside the kernel.
+    """
+    _on_gpu(x, qweight, scale, q_norm_w, k_norm_w, positions, cos_table, sin_table, slot_mapping, k_cache, v_cache)
+    _check(x.dtype == torch.bfloat16 and x.dim() == 2 and x.stride(-1) == 1, "qkv_rope_cache_rows: x")
+    n, k = qweight.shape
+    _check(n == (heads + 2 * kv_heads) * head_dim and x.shape[1] == k, "qkv_rope_cache_rows: qkv weight shape")
+    t = gather.numel() if gather is not None else x.shape[0]
+    _check(positions.dtype == torch.int64 and positions.numel() == t, "qkv_rope_cache_rows: positions")
+    _check(slot_mapping.dtype == torch.int64 and slot_mapping.numel() == t, "qkv_rope_cache_rows: slot_mapping")
+    _check(cos_table.dtype == torch.float32 and cos_table.is_contiguous() and cos_table.shape[-1] == head_dim, "cos")
+    _check(sin_table.shape == cos_table.shape and sin_table.is_contiguous(), "sin")
+    _check(k_cache.is_contiguous() and v_cache.is_contiguous() and k_cache.shape[-2:] == (kv_heads, head_dim), "caches")
+    if gather is not None:
+        _check(gather.dtype == torch.int64 and gather.is_contiguous(), "qkv_rope_cache_rows: gather")
+        _check(norm_w is not None, "qkv_rope_cache_rows: gathered rows need norm_w")
+    if x_copy is not None:
+        _check(x_copy.shape == (t, k) and x_copy.stride(-1) == 1, "qkv_rope_cache_rows: x_copy")
+    q = torch.empty(t, heads, head_dim, dtype=torch.bfloat16, device=x.device)
+    _native.call(
+        "msa_qkv_rope_cache_rows", _ptr(x), x.stride(0), x.shape[0], _ptr(gather), _ptr(norm_w), float(eps), _ptr(x_copy),
+        x_copy.stride(0) if x_copy is not None else 0, t, k, _ptr(qweight), _ptr(scale), heads, kv_heads, head_dim,
+        _ptr(q_norm_w), _ptr(k_norm_w), float(qk_eps), _ptr(positions), _ptr(cos_table), _ptr(sin_table),
+        cos_table.shape[0], _ptr(slot_mapping), _ptr(q), _ptr(k_cache), _ptr(v_cache), k_cache.shape[0], _stream(x),
+    )
+    return q
+
+
+def lm_head_argmax(
+    hidden: Tensor, rows: Tensor, norm_w: Tensor, eps: float, weight: Tensor, prenormed: bool = False
+) -> Tensor:
+    """Greedy next tokens of the sampled rows: argmax over bf16(RMSNorm(hidden[rows]) @ weight^T)
+    with the first index winning ties (model/qwen3.py:152-158 + runner/sampler.py:59); int64 [R].
+    ``prenormed``: hidden already holds the final norm's output (no RMSNorm is applied)."""
+    _on_gpu(hidden, rows, norm_w, weight)
+    _check(hidden.dtype == torch.bfloat16 and hidden.dim() == 2 and hidden.stride(-1) == 1, "lm_head_argmax: hidden")
+    _check(rows.dtype == torch.int64 and rows.is_contiguous(), "lm_head_argmax: rows must be int64")
+    _check(weight.dtype == torch.bfloat16 and weight.is_contiguous() and weight.shape[1] == hidden.shape[1],
+           "lm_head_argmax: weight [vocab, hidden] bf16")
+    r = rows.numel()
+    vocab, k = weight.shape
+    out = torch.empty(r, dtype=torch.int64, device=hidden.device)
+    ws_bytes = _native.query("msa_lm_head_argmax_workspace_size", r, vocab) if r else 0
+    ws = workspaces.get("lm_head", hidden.device, ws_bytes)
+    _native.call(
+        "msa_lm_head_argmax", _ptr(hidden), hidden.stride(0), hidden.shape[0], _ptr(rows), r, k,
+        _ptr(None if prenormed else norm_w),
+        float(eps), _ptr(weight),
+        vocab, _ptr(out), _ptr(ws), ws.numel() if ws is not None else 0, _stream(hidden),
     )
     return out

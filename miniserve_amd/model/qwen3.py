@@ -21,6 +21,7 @@ from dataclasses import dataclass
 from pathlib import Path
 from typing import Any
 
+import torch
 import torch.nn.functional as F
 from torch import Tensor, nn
 
@@ -150,16 +151,44 @@ class Qwen3ForCausalLM(nn.Module):
         meta: AttentionMetadata,
     ) -> Tensor:
         """input_ids, positions: [T]. Returns final hidden states [T, hidden] (qwen3.py:140-153)."""
-        x = self.embed_tokens(input_ids)
-        cos, sin = self.rotary(positions)
         if len(kv_caches) != len(self.layers):
             raise ValueError(f"{len(kv_caches)} KV caches for {len(self.layers)} layers")
+        if self._token_split_ok(input_ids.numel()):
+            residual = self._token_split_layers(input_ids, positions, kv_caches, meta)
+            out: Tensor = self.norm(residual)
+            return out
+        x = self.embed_tokens(input_ids)
+        cos, sin = self.rotary(positions)
         if self._all_int8():
             return self._fused_forward(x, cos, sin, kv_caches, meta)
         for layer, (k_cache, v_cache) in zip(self.layers, kv_caches, strict=True):
             x = layer(x, cos, sin, k_cache, v_cache, meta)
-        out: Tensor = self.norm(x)
+        out = self.norm(x)
         return out
+
+    def greedy(
+        self,
+        input_ids: Tensor,
+        positions: Tensor,
+        kv_caches: list[tuple[Tensor, Tensor]],
+        meta: AttentionMetadata,
+        logits_rows: Tensor,
+    ) -> Tensor:
+        """Greedy next token of each row in ``logits_rows``: the argmax of
+        ``compute_logits(forward(...)[logits_rows])`` (runner/model_runner.py:214-221 with
+        runner/sampler.py:59), with the final norm, LM head and argmax in one kernel pair."""
+        if len(kv_caches) != len(self.layers):
+            raise ValueError(f"{len(kv_caches)} KV caches for {len(self.layers)} layers")
+        weight = self.embed_tokens.weight if self.lm_head is None else self.lm_head.weight
+        if self._token_split_ok(input_ids.numel()):
+            residual = self._token_split_layers(input_ids, positions, kv_caches, meta)
+            return kernels.lm_head_argmax(residual, logits_rows, self.norm.weight, self.norm.eps, weight)
+        hidden = self.forward(input_ids, positions, kv_caches, meta)
+        rows = hidden[logits_rows]
+        if kernels.rows_supported(self.cfg.hidden_size) and rows.shape[0] > 0:
+            all_rows = torch.arange(rows.shape[0], device=rows.device)
+            return kernels.lm_head_argmax(rows, all_rows, self.norm.weight, self.norm.eps, weight, prenormed=True)
+        return self.compute_logits(rows).argmax(dim=-1)
 
     def _all_int8(self) -> bool:
         return all(
@@ -167,6 +196,52 @@ class Qwen3ForCausalLM(nn.Module):
             for layer in self.layers
             for m in (layer.self_attn.qkv_proj, layer.self_attn.o_proj, layer.mlp.gate_up_proj, layer.mlp.down_proj)
         )
+
+    def _token_split_ok(self, tokens: int) -> bool:
+        """Whether the token-split layer pipeline serves this batch: every linear int8, at most
+        ROWS_MAX_TOKENS tokens, head_dim 128 and the activation tiles within LDS."""
+        cfg = self.cfg
+        return (
+            0 < tokens <= kernels.ROWS_MAX_TOKENS
+            and cfg.head_dim == 128
+            and kernels.rows_supported(cfg.hidden_size)
+            and kernels.rows_supported(cfg.num_attention_heads * cfg.head_dim)
+            and kernels.rows_supported(cfg.intermediate_size)
+            and self._all_int8()
+        )
+
+    def _token_split_layers(
+        self, input_ids: Tensor, positions: Tensor, kv_caches: list[tuple[Tensor, Tensor]], meta: AttentionMetadata
+    ) -> Tensor:
+        """The layer loop on the token-split kernels, four launches plus attention per layer:
+          [embedding gather (layer 0) + input RMSNorm + int8 qkv + q/k-norm + RoPE + KV write]
+          -> paged attention -> [int8 o + residual add]
+          -> [post-attention RMSNorm + int8 gate_up + silu * up] -> [int8 down + residual add]
+        Returns the residual stream after the last layer (before the final norm)."""
+        cfg = self.cfg
+        t = input_ids.numel()
+        ids = input_ids if input_ids.dtype == torch.int64 and input_ids.is_contiguous() else input_ids.long().contiguous()
+        pos = positions if positions.dtype == torch.int64 and positions.is_contiguous() else positions.long().contiguous()
+        residual = torch.empty(t, cfg.hidden_size, dtype=torch.bfloat16, device=ids.device)
+        rot = self.rotary
+        for i, (layer, (k_cache, v_cache)) in enumerate(zip(self.layers, kv_caches, strict=True)):
+            attn, mlp = layer.self_attn, layer.mlp
+            qkv, o, gu, dn = attn.qkv_proj, attn.o_proj, mlp.gate_up_proj, mlp.down_proj
+            first = i == 0
+            q = kernels.qkv_rope_cache_rows(
+                self.embed_tokens.weight if first else residual, qkv.qweight, qkv.scale, attn.num_heads,
+                attn.num_kv_heads, attn.head_dim, attn.q_norm.weight, attn.k_norm.weight, attn.q_norm.eps, pos,
+                rot.cos, rot.sin, meta.slot_mapping, k_cache, v_cache, norm_w=layer.input_layernorm.weight,
+                eps=layer.input_layernorm.eps, gather=ids if first else None, x_copy=residual if first else None,
+            )
+            a = attend(q, k_cache, v_cache, meta, attn.scale).view(t, attn.q_size)
+            kernels.int8_linear_rows(a, o.qweight, o.scale, kernels.EPI_RESIDUAL, residual=residual, out=residual)
+            act = kernels.int8_linear_rows(
+                residual, gu.qweight, gu.scale, kernels.EPI_SILU_MUL,
+                norm_w=layer.post_attention_layernorm.weight, eps=layer.post_attention_layernorm.eps,
+            )
+            kernels.int8_linear_rows(act, dn.qweight, dn.scale, kernels.EPI_RESIDUAL, residual=residual, out=residual)
+        return residual
 
     def _fused_forward(
         self, x: Tensor, cos: Tensor, sin: Tensor, kv_caches: list[tuple[Tensor, Tensor]], meta: AttentionMetadata

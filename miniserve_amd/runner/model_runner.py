@@ -26,7 +26,6 @@ from torch import Tensor
 
 from miniserve_amd.attention.backends import AttentionMetadata, DecodePlan, SeqChunk, build_attention_metadata
 from miniserve_amd.model.qwen3 import Qwen3ForCausalLM
-from miniserve_amd.runner.sampler import sample
 from miniserve_amd.utils import to_device
 
 
@@ -59,6 +58,7 @@ class CapturedDecode:
         self.batch, self.max_blocks = batch, max_blocks
         self.host = torch.zeros(3 * batch + 2 * batch + batch * max_blocks, dtype=torch.int64, pin_memory=True)
         self.dev = torch.zeros_like(self.host, device=dev)
+        self.rows = torch.arange(batch, dtype=torch.int64, device=dev)  # every row is sampled
         b = batch
         self.ids, self.pos, self.slots = self.dev[:b], self.dev[b : 2 * b], self.dev[2 * b : 3 * b]
         meta32 = self.dev[3 * b :].view(torch.int32)  # q_rows | context_lens | tables, as int32
@@ -75,12 +75,11 @@ class CapturedDecode:
         stream.wait_stream(torch.cuda.current_stream(dev))
         with torch.cuda.stream(stream), torch.inference_mode():
             for _ in range(2):  # warm-up: reserves every workspace before capture
-                model.compute_logits(model(self.ids, self.pos, runner.kv_caches, self.meta)).argmax(dim=-1)
+                model.greedy(self.ids, self.pos, runner.kv_caches, self.meta, self.rows)
         torch.cuda.current_stream(dev).wait_stream(stream)
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph), torch.inference_mode():
-            hidden = model(self.ids, self.pos, runner.kv_caches, self.meta)
-            self.out_ids = model.compute_logits(hidden).argmax(dim=-1)
+            self.out_ids = model.greedy(self.ids, self.pos, runner.kv_caches, self.meta, self.rows)
 
     def run(self, scheduled: list[ScheduledChunk], block_size: int) -> list[int]:
         b = self.batch
@@ -175,6 +174,12 @@ class ModelRunner:
         return self.model.compute_logits(hidden[inp.logits_rows])
 
     @torch.inference_mode()
+    def forward_greedy(self, inp: StepInputs) -> Tensor:
+        """Greedy ids of the sampled rows, the same as ``sample(forward_logits(inp))`` without
+        materializing the logits (final norm, LM head and argmax fused)."""
+        return self.model.greedy(inp.input_ids, inp.positions, self.kv_caches, inp.attn, inp.logits_rows)
+
+    @torch.inference_mode()
     def execute(self, scheduled: list[ScheduledChunk]) -> list[list[int]]:
         """Run one step; return each scheduled sequence's new token ids (0 or 1 of them)."""
         results: list[list[int]] = [[] for _ in scheduled]
@@ -189,7 +194,7 @@ class ModelRunner:
         if inp.logits_rows.numel() == 0:
             self.model(inp.input_ids, inp.positions, self.kv_caches, inp.attn)
             return results
-        tokens = sample(self.forward_logits(inp)).tolist()  # the one device -> host sync
+        tokens = self.forward_greedy(inp).tolist()  # the one device -> host sync
         for j, idx in enumerate(inp.sample_idx):
             results[idx] = [tokens[j]]
         return results

@@ -77,6 +77,8 @@ def test_small_model_prefill_then_decode():
         assert rel_l2(got_logits, ref_logits) < 1e-2, step
         got_ids = got_logits.argmax(-1)
         assert torch.equal(got_ids, ref_ids) or float(_margins(ref_logits)[got_ids != ref_ids].max()) < 1e-2
+        fused = runner.forward_greedy(inp).cpu()  # final norm + LM head + argmax in one kernel pair
+        assert torch.equal(fused, ref_ids) or float(_margins(ref_logits)[fused != ref_ids].max()) < 1e-2
         seqs = [ScheduledChunk(s.token_ids + [int(ref_ids[i])], len(s.token_ids), 1, s.block_table)
                 for i, s in enumerate(seqs)]
 
@@ -215,9 +217,30 @@ def test_captured_decode_matches_eager(batch):
         ctx = rng.randint(1, 100)
         seqs.append(ScheduledChunk([rng.randrange(1024) for _ in range(ctx)], ctx - 1, 1, [8 * i + j for j in range(8)]))
     for step in range(4):
-        eager = runner.forward_logits(runner.prepare(seqs)).argmax(-1).tolist()
+        inp = runner.prepare(seqs)
+        eager = runner.forward_greedy(inp).tolist()
+        logits = runner.forward_logits(inp)
+        top2 = logits.topk(2, dim=-1).values
+        differ = [i for i, (e, a) in enumerate(zip(eager, logits.argmax(-1).tolist(), strict=True)) if e != a]
+        assert all(float(top2[i, 0] - top2[i, 1]) <= float(top2[i, 0].abs()) * 2.0**-7 for i in differ), differ
         torch.cuda.synchronize()
         graph = runner.execute(seqs)
         assert [g[0] for g in graph] == eager, step
         assert len(runner.graphs) == 1
         seqs = [ScheduledChunk(s.token_ids + [eager[i]], len(s.token_ids), 1, s.block_table) for i, s in enumerate(seqs)]
+
+
+def test_small_model_long_prefill_split_k_path():
+    """A 300-token prompt (above the token-split pipeline's 256-token limit) runs the split-K
+    layer pipeline and the prenormed LM-head path; logits and greedy ids match the oracle."""
+    runner, ocfg, ow, okv, tables = _pair(SMALL, seed=5, max_positions=512, num_blocks=40)
+    rng = random.Random(5)
+    toks = [rng.randrange(1024) for _ in range(300)]
+    sched = [ScheduledChunk(toks, 0, 300, list(range(19, -1, -1)))]
+    inp = runner.prepare(sched)
+    assert inp.input_ids.numel() > 256
+    got = runner.forward_logits(inp).cpu()
+    ref, ref_ids = _oracle_step(ocfg, ow, okv, tables, sched)
+    assert rel_l2(got, ref) < 1e-2
+    fused = runner.forward_greedy(inp).cpu()
+    assert torch.equal(fused, ref_ids) or float(_margins(ref)[fused != ref_ids].max()) < 1e-2
