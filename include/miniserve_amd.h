@@ -59,11 +59,21 @@ size_t msa_int8_linear_workspace_size(int64_t m, int64_t n, int64_t k);
  * multiplied on bf16 MFMA tiles with float32 accumulation. k % 16 == 0; x, qweight 16-byte
  * aligned. y has n columns (n/2 for MSA_EPI_SILU_MUL) with row stride ldy; residual (row stride
  * ldr) is read only for MSA_EPI_RESIDUAL and may alias y. When K is split across workgroups the
- * splits meet in the workspace and a second kernel sums them in a fixed order (deterministic). */
+ * splits meet in the workspace and a second kernel sums them in a fixed order (deterministic).
+ * Batches of 128 or more rows with k % 64 == 0 run msa_int8_gemm (no workspace). */
 int msa_int8_linear(const uint16_t* x, int64_t m, int64_t k, int64_t ldx, const int8_t* qweight,
                     const uint16_t* scale, int64_t n, uint16_t* y, int64_t ldy, int epilogue,
                     const uint16_t* residual, int64_t ldr, void* workspace, size_t workspace_bytes,
                     msa_stream_t stream);
+
+/* Int8Linear.forward (quant/int8.py:35-37) for prefill-sized batches: an LDS-tiled MFMA GEMM over
+ * 128-token x 128-row tiles; each int8 weight tile is dequantized once per token tile to the same
+ * bf16(q * s) value as the reference, float32 accumulation, then the epilogue of msa_int8_linear
+ * (MSA_EPI_RESIDUAL may write y in place over residual). k % 64 == 0; x, qweight 16-byte aligned.
+ * msa_int8_linear routes batches of 128 or more rows here. */
+int msa_int8_gemm(const uint16_t* x, int64_t m, int64_t k, int64_t ldx, const int8_t* qweight,
+                  const uint16_t* scale, int64_t n, uint16_t* y, int64_t ldy, int epilogue,
+                  const uint16_t* residual, int64_t ldr, msa_stream_t stream);
 
 /* The split-K half of Int8Linear.forward (quant/int8.py:35-37) for callers that fuse the
  * reduction into the next kernel: partials[s][m][n] (float32, k_split * m * n elements) holds the

@@ -16,7 +16,7 @@ from pathlib import Path
 import torch  # noqa: F401  -- must be imported before the HIP library is loaded
 
 LIB_PATH = Path(__file__).resolve().parent / "libminiserve_amd.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 # name -> (restype, argtypes); mirrors include/miniserve_amd.h.
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
@@ -28,6 +28,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         c_int,
         [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_int,
          c_void_p, c_int64, c_void_p, c_size_t, c_void_p],
+    ),
+    "msa_int8_gemm": (
+        c_int,
+        [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_int, c_void_p,
+         c_int64, c_void_p],
     ),
     "msa_int8_linear_splitk": (
         c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int, c_void_p, c_void_p]

@@ -61,6 +61,8 @@ __device__ __forceinline__ int decode_context(const DecodeArgs& a, int seq) {
 
 // Workgroup = W wavefronts for one (sequence, KV head, split). Wave w takes blocks b0 + w,
 // b0 + w + W, ... of the split, keeping the next block's K and V in flight while it computes one.
+// The grid is (KV head, split, sequence) with the KV head fastest, so the workgroups that read the
+// other head slices of the same token rows are dispatched together.
 //
 // Lane (rp, dg) = (lane / 8, lane % 8) owns key rows 2rp and 2rp + 1 of each 16-token block and
 // dims [8dg, 8dg + 8) and [64 + 8dg, 64 + 8dg + 8) of each row: one load instruction covers the
@@ -100,7 +102,7 @@ template <int G, int W>
 __global__ __launch_bounds__(64 * W) void paged_decode_kernel(DecodeArgs a) {
   __shared__ float s_acc[W][G][kHeadDim];
   __shared__ float s_ml[W][G][2];
-  const int split = blockIdx.x, seq = blockIdx.y, kvh = blockIdx.z;
+  const int kvh = blockIdx.x, split = blockIdx.y, seq = blockIdx.z;
   const int ctx = decode_context(a, seq);
   const int start = split * a.part_tokens;
   if (start >= ctx) return;  // the reduce kernel merges only splits that hold keys
@@ -442,11 +444,11 @@ extern "C" size_t msa_paged_attention_decode_workspace_size(int num_seqs, int he
 namespace msa {
 template <int G>
 static void launch_decode(const DecodeArgs& a, int num_seqs, hipStream_t s) {
-  // Four wavefronts per workgroup: at the kernel's register count (three or more wavefronts per
-  // SIMD for G <= 2) three workgroups share a CU, so a batch's (sequence, KV head) pairs are
-  // resident at once.
+  // Four wavefronts per workgroup: at the kernel's register count (three wavefronts per SIMD for
+  // G <= 2) three workgroups share a CU, so a batch's (sequence, KV head) pairs are resident at
+  // once.
   constexpr int W = 4;
-  const dim3 grid(a.splits, num_seqs, a.kv_heads);
+  const dim3 grid(a.kv_heads, a.splits, num_seqs);
   hipLaunchKernelGGL((paged_decode_kernel<G, W>), grid, dim3(64 * W), 0, s, a);
 }
 }  // namespace msa
@@ -463,8 +465,8 @@ extern "C" int msa_paged_attention_decode(const uint16_t* q, int64_t ldq, const 
     return fail(MSA_ERR_INVALID, "msa_paged_attention_decode: null pointer");
   if (head_dim != kHeadDim) return fail(MSA_ERR_UNSUPPORTED, "msa_paged_attention_decode: head_dim must be 128");
   if (block_size != kBlock) return fail(MSA_ERR_UNSUPPORTED, "msa_paged_attention_decode: block_size must be 16");
-  if (num_seqs < 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads != 0 || max_blocks <= 0)
-    return fail(MSA_ERR_INVALID, "msa_paged_attention_decode: bad shape");
+  if (num_seqs < 0 || num_seqs > 65535 || heads <= 0 || kv_heads <= 0 || heads % kv_heads != 0 || max_blocks <= 0)
+    return fail(MSA_ERR_INVALID, "msa_paged_attention_decode: bad shape (num_seqs <= 65535)");
   if (partition_tokens <= 0 || partition_tokens % kBlock != 0 || max_partitions <= 0 || max_partitions > 65535)
     return fail(MSA_ERR_INVALID, "msa_paged_attention_decode: partition_tokens must be a positive multiple of 16");
   if ((int64_t)partition_tokens * max_partitions < (int64_t)max_blocks * kBlock)

@@ -262,8 +262,16 @@ static int check_linear_args(const char* fn, const uint16_t* x, int64_t m, int64
 
 }  // namespace msa
 
+// Batches of at least this many rows (with k % 64 == 0) go to the LDS-tiled GEMM (gemm_int8.hip).
+constexpr int64_t kGemmMinRows = 128;
+
+extern "C" int msa_int8_gemm(const uint16_t* x, int64_t m, int64_t k, int64_t ldx, const int8_t* qweight,
+                             const uint16_t* scale, int64_t n, uint16_t* y, int64_t ldy, int epilogue,
+                             const uint16_t* residual, int64_t ldr, msa_stream_t stream);
+
 extern "C" size_t msa_int8_linear_workspace_size(int64_t m, int64_t n, int64_t k) {
   if (m <= 0 || n <= 0 || k <= 0) return 0;
+  if (m >= kGemmMinRows && k % 64 == 0) return 0;
   size_t best = 0;
   for (int epi = 0; epi < 3; ++epi) {
     const msa::SkinnyPlan p = msa::plan_skinny(m, n, k, epi, 0);
@@ -288,6 +296,8 @@ extern "C" int msa_int8_linear(const uint16_t* x, int64_t m, int64_t k, int64_t 
   if (ldy < out_cols) return fail(MSA_ERR_INVALID, "msa_int8_linear: ldy too small");
   if (epilogue == MSA_EPI_RESIDUAL && (!residual || ldr < n))
     return fail(MSA_ERR_INVALID, "msa_int8_linear: residual epilogue needs residual with ldr >= n");
+  if (m >= kGemmMinRows && k % 64 == 0)
+    return msa_int8_gemm(x, m, k, ldx, qweight, scale, n, y, ldy, epilogue, residual, ldr, stream);
 
   SkinnyPlan p = plan_skinny(m, n, k, epilogue, 0);
   const size_t need = p.k_split > 1 ? (size_t)p.k_split * m * n * sizeof(float) : 0;

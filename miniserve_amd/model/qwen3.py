@@ -5,13 +5,15 @@ Same module tree, parameter names and call signatures as the reference, so check
 loader's fused row order ([q | k | v] and [gate | up]) and the runner plug in unchanged, and each
 module's ``forward`` computes what the reference's does.
 
-Once every linear is int8, ``Qwen3ForCausalLM.forward`` runs the layers as one fused pipeline
-that crosses module boundaries (8 launches per layer, no workgroup ever waits on another):
-  int8 qkv (split-K partials) -> [sum + q/k-norm + RoPE + KV write] -> paged attention
-  -> int8 o (partials) -> [sum + residual add + post-attention RMSNorm]
-  -> int8 gate_up with silu*up epilogue -> int8 down (partials)
-  -> [sum + residual add + the NEXT layer's input RMSNorm (the final norm after the last layer)]
-Bracketed steps are single kernels. Logits are computed separately, only for sampled rows.
+Once every linear is int8, ``Qwen3ForCausalLM.forward`` runs the layers as fused pipelines that
+cross module boundaries (no workgroup ever waits on another):
+  * batches up to 256 tokens (decode steps, short chunks): the token-split kernels, five
+    launches per layer -- [embedding gather (layer 0) + input RMSNorm + int8 qkv + q/k-norm +
+    RoPE + KV write] -> [paged attention] -> [int8 o + residual] -> [post-attention RMSNorm +
+    int8 gate_up + silu * up] -> [int8 down + residual];
+  * larger batches (prefill chunks): the LDS-tiled int8 GEMM with residual / silu * up epilogues,
+    RMSNorm and q/k-norm + RoPE + KV write as their own kernels.
+Logits are computed only for sampled rows; ``greedy`` fuses the final norm, LM head and argmax.
 """
 
 from __future__ import annotations
@@ -246,28 +248,30 @@ class Qwen3ForCausalLM(nn.Module):
     def _fused_forward(
         self, x: Tensor, cos: Tensor, sin: Tensor, kv_caches: list[tuple[Tensor, Tensor]], meta: AttentionMetadata
     ) -> Tensor:
-        """The layer loop with every residual add / RMSNorm / split-K reduction fused into the
-        kernel that consumes it; returns norm(x_L), the same value as the module-by-module loop."""
+        """The layer loop for batches above the token-split limit (prefill chunks): int8 linears on
+        the LDS-tiled MFMA GEMM (residual adds and silu * up in its epilogue), RMSNorm and the
+        q/k-norm + RoPE + KV-write as their own kernels. Returns norm(x_L), the same value as the
+        module-by-module loop; ``x`` (the embedding output) is updated in place as the residual
+        stream."""
         cfg = self.cfg
-        eps = cfg.rms_norm_eps
         t = x.shape[0]
         layers = self.layers
-        h = kernels.rmsnorm(x, layers[0].input_layernorm.weight, eps)
+        h = kernels.rmsnorm(x, layers[0].input_layernorm.weight, layers[0].input_layernorm.eps)
         for i, (layer, (k_cache, v_cache)) in enumerate(zip(layers, kv_caches, strict=True)):
             attn, mlp = layer.self_attn, layer.mlp
             qkv, o, gu, dn = attn.qkv_proj, attn.o_proj, mlp.gate_up_proj, mlp.down_proj
-            part = kernels.int8_linear_splitk(h, qkv.qweight, qkv.scale, kernels.default_split(t, qkv.out_features, qkv.in_features))
-            q = kernels.qk_norm_rope_cache_splitk(
-                part, attn.num_heads, attn.num_kv_heads, attn.head_dim, attn.q_norm.weight, attn.k_norm.weight,
-                attn.q_norm.eps, cos, sin, meta.slot_mapping, k_cache, v_cache,
+            q = kernels.qk_norm_rope_cache(
+                kernels.int8_linear(h, qkv.qweight, qkv.scale), attn.num_heads, attn.num_kv_heads, attn.head_dim,
+                attn.q_norm.weight, attn.k_norm.weight, attn.q_norm.eps, cos, sin, meta.slot_mapping, k_cache, v_cache,
             )
             a = attend(q, k_cache, v_cache, meta, attn.scale).view(t, attn.q_size)
-            part = kernels.int8_linear_splitk(a, o.qweight, o.scale, kernels.default_split(t, o.out_features, o.in_features))
-            x, h = kernels.splitk_add_rmsnorm(part, x, layer.post_attention_layernorm.weight, eps)
-            act = gu(h, epilogue=kernels.EPI_SILU_MUL)
-            part = kernels.int8_linear_splitk(act, dn.qweight, dn.scale, kernels.default_split(t, dn.out_features, dn.in_features))
-            nxt = layers[i + 1].input_layernorm.weight if i + 1 < len(layers) else self.norm.weight
-            x, h = kernels.splitk_add_rmsnorm(part, x, nxt, eps)
+            kernels.int8_linear(a, o.qweight, o.scale, kernels.EPI_RESIDUAL, residual=x, out=x)
+            post = layer.post_attention_layernorm
+            act = kernels.int8_linear(kernels.rmsnorm(x, post.weight, post.eps), gu.qweight, gu.scale,
+                                      kernels.EPI_SILU_MUL)
+            kernels.int8_linear(act, dn.qweight, dn.scale, kernels.EPI_RESIDUAL, residual=x, out=x)
+            nxt = layers[i + 1].input_layernorm if i + 1 < len(layers) else self.norm
+            h = kernels.rmsnorm(x, nxt.weight, cfg.rms_norm_eps if nxt is self.norm else nxt.eps)
         return h
 
     def compute_logits(self, hidden: Tensor) -> Tensor:

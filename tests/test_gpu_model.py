@@ -230,8 +230,8 @@ def test_captured_decode_matches_eager(batch):
         seqs = [ScheduledChunk(s.token_ids + [eager[i]], len(s.token_ids), 1, s.block_table) for i, s in enumerate(seqs)]
 
 
-def test_small_model_long_prefill_split_k_path():
-    """A 300-token prompt (above the token-split pipeline's 256-token limit) runs the split-K
+def test_small_model_long_prefill_gemm_path():
+    """A 300-token prompt (above the token-split pipeline's 256-token limit) runs the GEMM
     layer pipeline and the prenormed LM-head path; logits and greedy ids match the oracle."""
     runner, ocfg, ow, okv, tables = _pair(SMALL, seed=5, max_positions=512, num_blocks=40)
     rng = random.Random(5)
