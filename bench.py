@@ -1,20 +1,26 @@
-"""Decode throughput of the int8 Qwen3-0.6B-shaped step at batch 64 on one MI355X.
+"""Throughput of MiniServe's int8 hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--workload NAME]
 
-Workload (one "step"): 64 sequences each decode one token; contexts 256 + U[0, 128] tokens in a
-paged KV pool of 16-token blocks (random permuted block tables, N(0,1) bf16 contents); a 28-layer
-Qwen3-0.6B-architecture model with random N(0, 0.02) bf16 weights, every decoder linear int8 per
-output channel, tied bf16 LM head. A step is what the runner does per engine step: build the flat
-batch and attention metadata on the host, upload it (pinned, non-blocking), run the forward, the
-LM head on the 64 sampled rows, greedy argmax, and the one device->host sync. The step runs as a
-captured HIP graph (one replay per step, metadata uploaded to its static buffers first).
+Default workload ``decode`` -- the headline metric: decode tok/s of a Qwen3-0.6B-architecture
+int8 model at batch 64. One step = what the runner does per engine step: build the flat batch and
+attention metadata on the host, upload it (pinned, non-blocking), run the 28 layers, the final
+norm + LM head + greedy argmax on the 64 sampled rows, and the one device->host sync; the step is
+a captured HIP graph replay. 64 sequences, contexts 256 + U[0, 128] in a paged KV pool of
+16-token blocks (permuted block tables, N(0, 1) bf16 contents); random N(0, 0.02) bf16 weights,
+every decoder linear int8 per output channel, tied bf16 LM head.
 
-Prints ONE JSON line. ``roofline`` is for the dominant kernel, paged-attention decode (76% of the
-step's bytes): algorithmic bytes per launch / its average duration, timed with HIP events on the
-stream it runs on over one launch per layer (28 distinct KV pools, so the Infinity Cache cannot
-serve repeats). ``cpu_baseline`` times the CPU oracle (a PyTorch restatement of the reference's
-path, run on this host's cores) on the same step.
+Other workloads (each prints its own JSON line):
+  linear     one int8 linear [3072 x 1024] (Qwen3-0.6B gate_proj) on 16 tokens -> GB/s
+  attention  paged-attention decode, 64 sequences, contexts U[128, 2048], 16 q / 8 KV heads -> GB/s
+  prefill    chunked-prefill step: one 1984-token prompt chunk + 64 decodes (contexts U[64, 1024])
+             on the same 0.6B model -> tok/s
+  decode8b   Qwen3-8B-shaped int8 decode, 256 tokens, contexts U[512, 4096] -> tok/s
+
+Every line carries ``roofline`` for the workload's dominant kernel (algorithmic bytes or flops per
+launch / its average duration, HIP events on the launch stream, inputs rotated past the 256 MB
+Infinity Cache) and ``cpu_baseline``: the CPU oracle (a PyTorch restatement of the reference's
+path) timed on this host's cores on a bounded sample of the same workload.
 """
 
 from __future__ import annotations
@@ -22,6 +28,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import platform
 import random
 import sys
 import time
@@ -32,22 +39,122 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "decode tok/s at batch 64 (Qwen3-0.6B int8); int8 GEMV + attn HBM GB/s vs peak"
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 BATCH, CTX_LO, CTX_HI = 64, 256, 384
+# FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 of one decode-attention launch on the decode workload, from
+# rocprofv3 --pmc (profiles/paged_decode_kernel_traffic_pmc.md); None until measured for this kernel.
+ATTN_TRAFFIC_BYTES: int | None = None
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_threads() -> int:
+    return min(len(os.sched_getaffinity(0)), 16)
+
+
+def hip_time(launch, count: int, reps: int = 3) -> float:
+    """Seconds per launch: ``launch(i)`` for i < count queued back to back behind a spin kernel,
+    bracketed by HIP events on the current stream (the stream the kernels are launched on);
+    the best of ``reps`` passes after one warm-up pass."""
+    import torch
+
+    for i in range(count):
+        launch(i)
+    torch.cuda.synchronize()
+    best = float("inf")
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(5_000_000)
+        e0.record()
+        for i in range(count):
+            launch(i)
+        e1.record()
+        torch.cuda.synchronize()
+        best = min(best, e0.elapsed_time(e1) * 1e-3 / count)
+    return best
+
+
+def cpu_time(fn, budget_s: float = 20.0, max_reps: int = 5) -> tuple[float, int]:
+    """Median seconds of ``fn()`` on the host after one warm-up, as many runs as fit the budget."""
+    t = time.perf_counter()
+    fn()
+    first = time.perf_counter() - t
+    reps = max(1, min(max_reps, int(budget_s / max(first, 1e-6))))
+    times = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t)
+    times.sort()
+    return times[len(times) // 2], reps
+
+
+def cpu_fields(value: float, unit: str, sample: str) -> dict:
+    import torch
+
+    return {"value": round(value, 3), "unit": unit, "cores": cpu_threads(), "kind": "port", "sample": sample,
+            "cpu": platform.processor() or platform.machine(), "torch": torch.__version__}
+
+
+def roofline(kernel: str, bound: str, achieved: float, per_launch: int, secs: float, traffic=None) -> dict:
+    peak, unit = (HBM_PEAK_GBS, "GB/s") if bound == "hbm" else (MFMA_BF16_PEAK_TFLOPS, "TFLOP/s")
+    out = {"kernel": kernel, "bound": bound, "achieved": round(achieved, 1), "peak": peak, "unit": unit,
+           "frac": round(achieved / peak, 4), "traffic": traffic, "us_per_launch": round(secs * 1e6, 3)}
+    out["bytes_per_launch" if bound == "hbm" else "flops_per_launch"] = per_launch
+    return out
+
+
+def line(metric: str, value: float, unit: str, args, ms: float, config: dict, higher: bool = True) -> dict:
+    return {"metric": metric, "value": round(value, 1), "unit": unit, "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": higher, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16", "data": "synthetic", "config": config}
+
+
+# ---- algorithmic work per unit ---------------------------------------------------------------------
 
 
 def attention_bytes(ctx: list[int], heads: int, kv_heads: int, dim: int) -> int:
-    """Algorithmic bytes of one decode-attention launch: every context token's K and V for every
-    KV head, the queries and outputs, the block-table entries read and the per-sequence ints."""
+    """One decode-attention launch: every context token's K and V for every KV head, the queries
+    and outputs, the block-table entries read and the per-sequence ints."""
     kv = 2 * kv_heads * dim * 2 * sum(ctx)
     qo = 2 * len(ctx) * heads * dim * 2
     tables = 4 * sum(-(-c // 16) for c in ctx)
     return kv + qo + tables + 8 * len(ctx)
 
 
-def time_attention(runner, sched, cfg, reps: int = 4) -> tuple[float, int]:
-    """Average duration of the dominant kernel: one decode-attention launch per layer (28
-    distinct KV pools) queued back to back behind a spin kernel, timed by one pair of HIP events
-    on the stream the launches go to; returns (seconds per launch, algorithmic bytes per launch)."""
+def linear_bytes(m: int, n: int, k: int) -> int:
+    """One int8 linear: int8 weights, bf16 scales, bf16 x in, bf16 y out."""
+    return n * k + 2 * n + 2 * m * k + 2 * m * n
+
+
+# ---- shared model setup -----------------------------------------------------------------------------
+
+
+def build_int8_model(cfg: dict, seed: int, dev, max_positions: int, on_device: bool = False):
+    from miniserve_amd import workloads
+    from miniserve_amd.quant.int8 import quantize_int8_
+
+    weights = workloads.random_weights(cfg, seed=seed, device="cuda" if on_device else "cpu")
+    model = workloads.build_model(cfg, weights, dev, max_positions=max_positions)
+    quantize_int8_(model)
+    return model, weights
+
+
+def decode_sched(cfg: dict, batch, seed: int):
+    from miniserve_amd.runner.model_runner import ScheduledChunk
+
+    rng = random.Random(seed)
+    sched = []
+    for c, table, tok in zip(batch.context_lens, batch.block_tables, batch.token_ids, strict=True):
+        sched.append(ScheduledChunk([rng.randrange(cfg["vocab_size"]) for _ in range(c - 1)] + [tok], c - 1, 1, table))
+    return sched
+
+
+def time_layer_attention(runner, sched, cfg) -> tuple[float, int, str]:
+    """The dominant decode kernel: one decode-attention launch per layer (distinct KV pools) per
+    pass; returns (seconds per launch, algorithmic bytes per launch, kernel name)."""
     import torch
 
     from miniserve_amd import kernels
@@ -58,103 +165,345 @@ def time_attention(runner, sched, cfg, reps: int = 4) -> tuple[float, int]:
     ptok, parts = kernels.decode_splits(d.num_seqs, kvh, d.block_tables.shape[1])
     q = torch.randn(len(sched), heads, dim, device=runner.device).to(torch.bfloat16)
     out = torch.empty_like(q)
-    spans = []
-    for rep in range(reps):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda._sleep(20_000_000)
-        e0.record()
-        for kc, vc in runner.kv_caches:
-            kernels.paged_attention_decode(q, kc, vc, d.block_tables, d.context_lens, d.q_rows, ptok, parts,
-                                           dim**-0.5, out)
-        e1.record()
-        torch.cuda.synchronize()
-        if rep:
-            spans.append(e0.elapsed_time(e1) * 1e-3 / len(runner.kv_caches))
+    caches = runner.kv_caches
+
+    def launch(i):
+        kc, vc = caches[i]
+        kernels.paged_attention_decode(q, kc, vc, d.block_tables, d.context_lens, d.q_rows, ptok, parts, dim**-0.5, out)
+
+    secs = hip_time(launch, len(caches), reps=4)
     ctx = [s.num_computed + 1 for s in sched]
-    return sum(spans) / len(spans), attention_bytes(ctx, heads, kvh, dim)
+    return secs, attention_bytes(ctx, heads, kvh, dim), f"paged_decode_kernel<{heads // kvh}, 4>"
 
 
-def linear_bytes(m: int, n: int, k: int) -> int:
-    """Algorithmic bytes of one int8 linear: int8 weights, bf16 scales, bf16 x in, bf16 y out."""
-    return n * k + 2 * n + 2 * m * k + 2 * m * n
+def time_graph_steps(runner, sched, steps: int, warmup: int) -> float:
+    import torch
+
+    for _ in range(warmup):
+        runner.execute(sched)
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    for _ in range(steps):
+        runner.execute(sched)
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t) / steps
 
 
-def time_linears(seed: int) -> list[dict]:
-    """Average duration of the token-split int8 linear on the single gate_proj-shaped linear
-    ([3072 x 1024], 16 tokens) and on the four decode-step linears at 64 tokens, each over enough
-    distinct weight copies (> 256 MiB) that the Infinity Cache cannot serve repeats; HIP events on
-    the launch stream around one pass over the copies, after a warm-up pass."""
+# ---- workloads ------------------------------------------------------------------------------------
+
+
+def bench_decode(args) -> dict:
+    import torch
+
+    from miniserve_amd import workloads
+    from miniserve_amd.runner.model_runner import ModelRunner
+
+    dev = torch.device("cuda:0")
+    cfg = workloads.QWEN3_0_6B
+    t0 = time.time()
+    model, weights = build_int8_model(cfg, args.seed, dev, 4096)
+    batch = workloads.decode_batch(BATCH, CTX_LO, CTX_HI, seed=args.seed + 1, vocab=cfg["vocab_size"], spare_blocks=64)
+    runner = ModelRunner(model, dev, use_graphs=True, max_model_len=4096)
+    runner.allocate_kv_cache(batch.num_blocks)
+    workloads.fill_kv_pool_(runner.kv_cache, seed=args.seed + 2, on_device=True)
+    sched = decode_sched(cfg, batch, args.seed + 3)
+    torch.cuda.synchronize()
+    log(f"setup {time.time() - t0:.1f}s: 28-layer int8 model, {batch.num_blocks} KV blocks")
+
+    def eager_step() -> list[int]:
+        return runner.forward_greedy(runner.prepare(sched)).tolist()
+
+    for _ in range(2):
+        eager_step()
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    n_eager = max(3, args.steps // 4)
+    for _ in range(n_eager):
+        eager_step()
+    torch.cuda.synchronize()
+    eager_dt = (time.perf_counter() - t) / n_eager
+    graph_ids = runner.execute(sched)
+    if [g[0] for g in graph_ids] != eager_step():
+        raise RuntimeError("captured decode step disagrees with the eager step")
+    dt = time_graph_steps(runner, sched, args.steps, args.warmup)
+    log(f"eager {eager_dt * 1e3:.3f} ms/step; graph {args.steps} steps: {dt * 1e3:.3f} ms/step, {BATCH / dt:.0f} tok/s")
+    secs, nbytes, kname = time_layer_attention(runner, sched, cfg)
+    log(f"decode attention: {secs * 1e6:.2f} us/launch, {nbytes / secs / 1e9:.0f} GB/s")
+    out = line(METRIC, BATCH / dt, "tok/s", args, dt * 1e3, {
+        "workload": "Qwen3-0.6B-architecture int8 decode step (28 layers, random init)",
+        "batch": BATCH, "context": f"{CTX_LO}+U[0,{CTX_HI - CTX_LO}]", "sum_context": sum(batch.context_lens),
+        "kv_block": 16, "weights": "int8 per-output-channel, bf16 activations, fp32 accumulation, tied bf16 LM head",
+        "parallelism": "none", "hip_graph": True, "eager_ms_per_step": round(eager_dt * 1e3, 4)})
+    out["roofline"] = roofline(kname, "hbm", nbytes / secs / 1e9, nbytes, secs, ATTN_TRAFFIC_BYTES)
+    if not args.no_cpu_baseline:
+        from oracle import model as om
+
+        torch.set_num_threads(cpu_threads())
+        ocfg = om.Config.from_dict(cfg)
+        ow = om.quantize_weights(weights, ocfg)
+        okv = [(kc.cpu(), vc.cpu()) for kc, vc in runner.kv_caches]
+        tables = om.tables_for(ocfg, 4096)
+        step = om.prepare([(s.token_ids, s.num_computed, s.num_new, s.block_table) for s in sched], 16)
+        med, reps = cpu_time(lambda: om.run_step(ocfg, ow, okv, step, 16, tables))
+        log(f"cpu oracle: {med:.3f} s/step on {cpu_threads()} threads")
+        out["cpu_baseline"] = cpu_fields(BATCH / med, "tok/s", "the full decode step (64 tokens, 28 layers, LM head, "
+                                         f"argmax), median of {reps} after 1 warm-up")
+    return out
+
+
+def bench_linear(args) -> dict:
     import torch
 
     from miniserve_amd import kernels
 
     dev = torch.device("cuda:0")
-    g = torch.Generator(device=dev).manual_seed(seed)
-    shapes = [("gate_proj [3072x1024], 16 tokens", 16, 3072, 1024, kernels.EPI_NONE),
-              ("qkv [4096x1024] + q/k-norm/RoPE/cache, 64 tokens", 64, 4096, 1024, -1),
-              ("o [1024x2048] + residual, 64 tokens", 64, 1024, 2048, kernels.EPI_RESIDUAL),
-              ("gate_up [6144x1024] + norm + silu*up, 64 tokens", 64, 6144, 1024, kernels.EPI_SILU_MUL),
-              ("down [1024x3072] + residual, 64 tokens", 64, 1024, 3072, kernels.EPI_RESIDUAL)]
-    out = []
-    for name, m, n, k, epi in shapes:
-        copies = max(8, -(-(300 << 20) // (n * k)))
-        ws = torch.randint(-127, 128, (copies, n, k), dtype=torch.int8, device=dev, generator=g)
-        sc = (torch.rand(copies, n, device=dev, generator=g) * 0.001).to(torch.bfloat16)
-        x = torch.randn(m, k, device=dev, generator=g).to(torch.bfloat16)
-        nw = torch.ones(k, dtype=torch.bfloat16, device=dev)
-        resid = torch.randn(m, n, device=dev, generator=g).to(torch.bfloat16)
-        y = torch.empty(m, n // 2 if epi == kernels.EPI_SILU_MUL else n, dtype=torch.bfloat16, device=dev)
-        if epi == -1:
-            heads, kvh = 16, 8
-            pos = torch.arange(m, device=dev) + 300
-            cos = torch.randn(4096, 128, device=dev)
-            sin = torch.randn(4096, 128, device=dev)
-            slots = torch.arange(m, device=dev)
-            kc = torch.zeros(m, kvh, 128, dtype=torch.bfloat16, device=dev)
-            vc = torch.zeros_like(kc)
+    m, n, k = 16, 3072, 1024
+    copies = -(-(300 << 20) // (n * k))  # > 256 MB of distinct weights
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    qs = []
+    for _ in range(copies):
+        w = (torch.randn(n, k, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        qs.append(kernels.int8_quantize(w))
+    x = torch.randn(m, k, generator=g, device=dev).to(torch.bfloat16)
+    y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
 
-            def run(i):
-                kernels.qkv_rope_cache_rows(x, ws[i], sc[i], heads, kvh, 128, nw[:128], nw[:128], 1e-6, pos, cos, sin,
-                                            slots, kc, vc, norm_w=nw, eps=1e-6)
-        elif epi == kernels.EPI_SILU_MUL:
-            def run(i):
-                kernels.int8_linear_rows(x, ws[i], sc[i], epi, norm_w=nw, eps=1e-6, out=y)
-        elif epi == kernels.EPI_RESIDUAL:
-            def run(i):
-                kernels.int8_linear_rows(x, ws[i], sc[i], epi, residual=resid, out=y)
-        else:
-            def run(i):
-                kernels.int8_linear_rows(x, ws[i], sc[i], out=y)
-        for i in range(copies):
-            run(i)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda._sleep(5_000_000)
-        e0.record()
-        for i in range(copies):
-            run(i)
-        e1.record()
-        torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) * 1e3 / copies
-        nbytes = linear_bytes(m, n, k)
-        out.append({"linear": name, "us_per_launch": round(us, 3), "bytes_per_launch": nbytes,
-                    "GB_s": round(nbytes / us / 1e3, 1), "copies": copies})
-        del ws, sc
+    def launch(i):
+        kernels.int8_linear(x, qs[i][0], qs[i][1], out=y)
+
+    secs = hip_time(launch, copies)
+    nbytes = linear_bytes(m, n, k)
+    gbs = nbytes / secs / 1e9
+    log(f"int8 linear [{n}x{k}] x {m}: {secs * 1e6:.2f} us/launch, {gbs:.0f} GB/s")
+    out = line("int8 linear [3072x1024] x 16 tokens: algorithmic HBM GB/s", gbs, "GB/s", args, secs * 1e3, {
+        "workload": "single int8 weight-only linear, Qwen3-0.6B gate_proj shape", "tokens": m, "out_features": n,
+        "in_features": k, "weights": "N(0,0.02) bf16 quantized per output channel", "copies_rotated": copies})
+    out["roofline"] = roofline("int8_rows_kernel<1, 1, 8, 8, 0, 0>", "hbm", gbs, nbytes, secs)
+    if not args.no_cpu_baseline:
+        from oracle import int8 as oi
+
+        torch.set_num_threads(cpu_threads())
+        xc, qc, sc = x.cpu(), qs[0][0].cpu(), qs[0][1].cpu()
+        med, reps = cpu_time(lambda: oi.int8_linear(xc, qc, sc), budget_s=10.0, max_reps=200)
+        out["cpu_baseline"] = cpu_fields(nbytes / med / 1e9, "GB/s", f"the same linear on the CPU oracle (whole-matrix "
+                                         f"dequantization + F.linear), median of {reps}")
     return out
 
 
-def kernel_only(mode: str, seed: int) -> int:
-    """Profiling entry points: ``attention`` runs only the decode-attention timing above on the
-    bench workload; ``linear`` the int8 linear timings of ``time_linears``; ``copy`` copies a
-    256 MiB buffer 10 times (a kernel of known traffic, to calibrate rocprofv3's FETCH_SIZE /
-    WRITE_SIZE counters)."""
+def bench_attention(args) -> dict:
     import torch
 
+    from miniserve_amd import kernels, workloads
+    from miniserve_amd.attention import backends as hb
+
     dev = torch.device("cuda:0")
-    if mode == "linear":
-        for row in time_linears(seed):
-            print(json.dumps(row))
-        return 0
+    nseq, heads, kvh, dim = 64, 16, 8, 128
+    b = workloads.decode_batch(nseq, 128, 2048, seed=args.seed + 1, spare_blocks=0)
+    pools = 4  # 4 x ~286 MB of K/V: repeats cannot come from the Infinity Cache
+    kv = torch.empty(pools, 2, b.num_blocks * 16, kvh, dim, dtype=torch.bfloat16, device=dev)
+    workloads.fill_kv_pool_(kv, seed=args.seed + 2, on_device=True)
+    g = torch.Generator(device=dev).manual_seed(args.seed + 3)
+    q = torch.randn(nseq, heads, dim, generator=g, device=dev).to(torch.bfloat16)
+    knew = torch.randn(nseq, kvh, dim, generator=g, device=dev).to(torch.bfloat16)
+    vnew = torch.randn(nseq, kvh, dim, generator=g, device=dev).to(torch.bfloat16)
+    slots = torch.tensor(b.slot_mapping, dtype=torch.int64, device=dev)
+    chunks = [hb.SeqChunk(i, 1, c - 1, t) for i, (c, t) in enumerate(zip(b.context_lens, b.block_tables, strict=True))]
+    meta = hb.build_attention_metadata(chunks, slots, 16)
+    scale = dim**-0.5
+
+    def op(i):
+        hb.paged_attention(q, knew, vnew, kv[i % pools, 0], kv[i % pools, 1], meta, scale)
+
+    op_secs = hip_time(op, 2 * pools)
+    ctx = b.context_lens
+    op_bytes = 4096 * sum(ctx) + 786_432 + 4 * sum(-(-c // 16) for c in ctx) + 256
+    d = meta.decode
+    ptok, parts = kernels.decode_splits(nseq, kvh, d.block_tables.shape[1])
+    out_t = torch.empty_like(q)
+
+    def kern(i):
+        kernels.paged_attention_decode(q, kv[i % pools, 0], kv[i % pools, 1], d.block_tables, d.context_lens, d.q_rows,
+                                       ptok, parts, scale, out_t)
+
+    k_secs = hip_time(kern, 2 * pools)
+    k_bytes = attention_bytes(ctx, heads, kvh, dim)
+    log(f"paged_attention (write + attend): {op_secs * 1e6:.2f} us, {op_bytes / op_secs / 1e9:.0f} GB/s; "
+        f"decode kernel {k_secs * 1e6:.2f} us, {k_bytes / k_secs / 1e9:.0f} GB/s")
+    out = line("paged-attention decode GB/s (64 seqs, ctx U[128,2048], 16q/8kv, d=128)", op_bytes / op_secs / 1e9,
+               "GB/s", args, op_secs * 1e3, {
+                   "workload": "paged_attention: KV write + decode attention through permuted 16-token block tables",
+                   "seqs": nseq, "sum_context": sum(ctx), "heads": heads, "kv_heads": kvh, "head_dim": dim,
+                   "bytes_per_call": op_bytes, "pools_rotated": pools})
+    out["roofline"] = roofline(f"paged_decode_kernel<{heads // kvh}, 4>", "hbm", k_bytes / k_secs / 1e9, k_bytes, k_secs)
+    if not args.no_cpu_baseline:
+        from oracle import attention as oa
+
+        torch.set_num_threads(cpu_threads())
+        kc, vc = kv[0, 0].cpu(), kv[0, 1].cpu()
+        qc, kn, vn, sl = q.cpu(), knew.cpu(), vnew.cpu(), slots.cpu()
+        ometa = oa.build_attention_metadata([oa.SeqChunk(*c.__dict__.values()) for c in chunks], sl, 16)
+        med, reps = cpu_time(lambda: oa.paged_attention(qc, kn, vn, kc, vc, ometa, scale), budget_s=20.0)
+        out["cpu_baseline"] = cpu_fields(op_bytes / med / 1e9, "GB/s", f"the same paged_attention call on the CPU "
+                                         f"oracle (gather + SDPA), median of {reps}")
+    return out
+
+
+def bench_prefill(args) -> dict:
+    import torch
+
+    from miniserve_amd import kernels, workloads
+    from miniserve_amd.runner.model_runner import ModelRunner, ScheduledChunk
+
+    dev = torch.device("cuda:0")
+    cfg = workloads.QWEN3_0_6B
+    model, weights = build_int8_model(cfg, args.seed, dev, 4096)
+    dec = workloads.decode_batch(64, 64, 1024, seed=args.seed + 1, vocab=cfg["vocab_size"], spare_blocks=0)
+    chunk = 1984
+    pblocks = -(-chunk // 16)
+    total_blocks = dec.num_blocks + pblocks
+    runner = ModelRunner(model, dev, use_graphs=False, max_model_len=4096)
+    runner.allocate_kv_cache(total_blocks)
+    workloads.fill_kv_pool_(runner.kv_cache, seed=args.seed + 2, on_device=True)
+    sched = decode_sched(cfg, dec, args.seed + 3)
+    rng = random.Random(args.seed + 4)
+    prompt = [rng.randrange(cfg["vocab_size"]) for _ in range(chunk)]
+    sched.append(ScheduledChunk(prompt, 0, chunk, list(range(dec.num_blocks, total_blocks))))
+    tokens = sum(s.num_new for s in sched)
+    for _ in range(args.warmup):
+        runner.execute(sched)
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    for _ in range(args.steps):
+        runner.execute(sched)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t) / args.steps
+    log(f"chunked-prefill step ({tokens} tokens): {dt * 1e3:.3f} ms/step, {tokens / dt:.0f} tok/s")
+    # dominant kernel: the gate_up GEMM at M = 2048 over the 28 layers' weights
+    h = torch.randn(tokens, cfg["hidden_size"], device=dev).to(torch.bfloat16)
+    y = torch.empty(tokens, cfg["intermediate_size"], dtype=torch.bfloat16, device=dev)
+    lin = [layer.mlp.gate_up_proj for layer in model.layers]
+
+    def launch(i):
+        kernels.int8_linear(h, lin[i].qweight, lin[i].scale, kernels.EPI_SILU_MUL, out=y)
+
+    secs = hip_time(launch, len(lin))
+    flops = 2 * tokens * 2 * cfg["intermediate_size"] * cfg["hidden_size"]
+    log(f"gate_up GEMM M={tokens}: {secs * 1e6:.1f} us, {flops / secs / 1e12:.1f} TFLOP/s")
+    sum_dec = sum(dec.context_lens)
+    step_flops = (2 * tokens * 15_728_640 * 28 + 4 * 16 * 128 * (chunk * (chunk + 1) // 2) * 28
+                  + 8192 * sum_dec * 28 + 2 * 65 * 1024 * cfg["vocab_size"])
+    out = line("chunked-prefill step tok/s (1984-token chunk + 64 decodes, Qwen3-0.6B int8)", tokens / dt, "tok/s", args,
+               dt * 1e3, {"workload": "mixed flat batch: 64 decodes (contexts U[64,1024]) first, then one fresh "
+                          "1984-token prompt chunk; eager step (prepare + forward + fused LM head/argmax + sync)",
+                          "tokens": tokens, "step_tflop": round(step_flops / 1e12, 3),
+                          "step_tflop_s": round(step_flops / dt / 1e12, 1)})
+    out["roofline"] = roofline("int8_gemm_kernel<SILU_MUL> (gate_up, M=2048)", "mfma", flops / secs / 1e12, flops, secs)
+    if not args.no_cpu_baseline:
+        from oracle import model as om
+        from oracle.attention import build_attention_metadata as oracle_meta
+
+        torch.set_num_threads(cpu_threads())
+        ocfg = om.Config.from_dict(cfg)
+        ow = om.quantize_weights({k: v for k, v in weights.items() if k.startswith("layers.0.") or "layers." not in k},
+                                 om.Config.from_dict({**cfg, "num_hidden_layers": 1}))
+        step = om.prepare([(s.token_ids, s.num_computed, s.num_new, s.block_table) for s in sched], 16)
+        ometa = oracle_meta(step.chunks, step.slot_mapping, 16)
+        kc, vc = runner.kv_caches[0][0].cpu(), runner.kv_caches[0][1].cpu()
+        tables = om.tables_for(ocfg, 4096)
+        x0 = torch.nn.functional.embedding(step.input_ids, ow["embed_tokens.weight"])
+        cos, sin = tables[0][step.positions], tables[1][step.positions]
+
+        def one_layer():
+            with torch.inference_mode():
+                om.decoder_layer(ocfg, ow, 0, x0, cos, sin, kc, vc, ometa)
+
+        def head():
+            with torch.inference_mode():
+                om.greedy(om.compute_logits(ocfg, ow, x0[step.logits_rows]))
+
+        lay, reps = cpu_time(one_layer, budget_s=20.0, max_reps=3)
+        hd, _ = cpu_time(head, budget_s=5.0, max_reps=3)
+        est = 28 * lay + hd
+        out["cpu_baseline"] = cpu_fields(tokens / est, "tok/s", f"one decoder layer of this step on the CPU oracle "
+                                         f"(median of {reps}) x 28 + the LM head and argmax of its 65 sampled rows")
+    return out
+
+
+def bench_decode8b(args) -> dict:
+    import torch
+
+    from miniserve_amd import workloads
+    from miniserve_amd.runner.model_runner import ModelRunner
+
+    dev = torch.device("cuda:0")
+    cfg = workloads.QWEN3_8B
+    nseq = 256
+    t0 = time.time()
+    model, weights = build_int8_model(cfg, args.seed, dev, 4096 + 16, on_device=True)
+    keep = {k: v.cpu() for k, v in weights.items() if k.startswith("layers.0.") or "layers." not in k}
+    del weights
+    torch.cuda.empty_cache()
+    batch = workloads.decode_batch(nseq, 512, 4096, seed=args.seed + 1, vocab=cfg["vocab_size"], spare_blocks=0)
+    runner = ModelRunner(model, dev, use_graphs=True, max_model_len=4096 + 16)
+    runner.allocate_kv_cache(batch.num_blocks)
+    workloads.fill_kv_pool_(runner.kv_cache, seed=args.seed + 2, on_device=True)
+    sched = decode_sched(cfg, batch, args.seed + 3)
+    torch.cuda.synchronize()
+    log(f"setup {time.time() - t0:.1f}s: 36-layer 8B-shaped int8 model, {batch.num_blocks} KV blocks "
+        f"({runner.kv_cache.numel() * 2 / 1e9:.1f} GB)")
+    dt = time_graph_steps(runner, sched, args.steps, args.warmup)
+    log(f"graph {args.steps} steps: {dt * 1e3:.3f} ms/step, {nseq / dt:.0f} tok/s")
+    secs, nbytes, kname = time_layer_attention(runner, sched, cfg)
+    log(f"decode attention: {secs * 1e6:.2f} us/launch, {nbytes / secs / 1e9:.0f} GB/s")
+    out = line("decode tok/s at batch 256 (Qwen3-8B-shaped int8, contexts U[512,4096])", nseq / dt, "tok/s", args,
+               dt * 1e3, {"workload": "Qwen3-8B-architecture int8 decode step (36 layers, untied bf16 LM head, "
+                          "random init)", "batch": nseq, "sum_context": sum(batch.context_lens), "kv_block": 16,
+                          "hip_graph": True})
+    out["roofline"] = roofline(kname, "hbm", nbytes / secs / 1e9, nbytes, secs)
+    if not args.no_cpu_baseline:
+        from oracle import model as om
+        from oracle.attention import build_attention_metadata as oracle_meta
+
+        torch.set_num_threads(cpu_threads())
+        ocfg = om.Config.from_dict(cfg)
+        ow = om.quantize_weights(keep, om.Config.from_dict({**cfg, "num_hidden_layers": 1}))
+        step = om.prepare([(s.token_ids, s.num_computed, s.num_new, s.block_table) for s in sched], 16)
+        ometa = oracle_meta(step.chunks, step.slot_mapping, 16)
+        kc, vc = runner.kv_caches[0][0].cpu(), runner.kv_caches[0][1].cpu()
+        tables = om.tables_for(ocfg, 4096 + 16)
+        x0 = torch.nn.functional.embedding(step.input_ids, ow["embed_tokens.weight"])
+        cos, sin = tables[0][step.positions], tables[1][step.positions]
+        rows = 16  # LM-head sample: 16 of the 256 sampled rows, scaled by 16
+
+        def one_layer():
+            with torch.inference_mode():
+                om.decoder_layer(ocfg, ow, 0, x0, cos, sin, kc, vc, ometa)
+
+        def head():
+            with torch.inference_mode():
+                om.greedy(om.compute_logits(ocfg, ow, x0[:rows]))
+
+        lay, reps = cpu_time(one_layer, budget_s=20.0, max_reps=3)
+        hd, _ = cpu_time(head, budget_s=10.0, max_reps=3)
+        est = 36 * lay + hd * (nseq / rows)
+        out["cpu_baseline"] = cpu_fields(nseq / est, "tok/s", f"one decoder layer of this step on the CPU oracle "
+                                         f"(median of {reps}) x 36 + the LM head/argmax of 16 rows x 16")
+    return out
+
+
+# ---- profiling entry points -----------------------------------------------------------------------
+
+
+def kernel_only(mode: str, seed: int) -> int:
+    """``attention``: only the decode-attention timing of the decode workload; ``linear``: the int8
+    linears of the decode step (plus the single gate_proj-shaped linear) over rotated weights;
+    ``copy``: a 256 MiB copy, 10 times (a kernel of known traffic, to calibrate rocprofv3's
+    FETCH_SIZE / WRITE_SIZE)."""
+    import torch
+
+    from miniserve_amd import kernels, workloads
+    from miniserve_amd.runner.model_runner import ModelRunner
+
+    dev = torch.device("cuda:0")
     if mode == "copy":
         src = torch.empty(128 << 20, dtype=torch.bfloat16, device=dev).normal_()
         dst = torch.empty_like(src)
@@ -163,23 +512,63 @@ def kernel_only(mode: str, seed: int) -> int:
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_each_way": src.numel() * 2, "copies": 10}))
         return 0
-    from miniserve_amd import workloads
-    from miniserve_amd.runner.model_runner import ModelRunner, ScheduledChunk
+    if mode == "linear":
+        g = torch.Generator(device=dev).manual_seed(seed)
+        shapes = [("gate_proj [3072x1024], 16 tokens", 16, 3072, 1024, kernels.EPI_NONE),
+                  ("qkv [4096x1024] + q/k-norm/RoPE/cache, 64 tokens", 64, 4096, 1024, -1),
+                  ("o [1024x2048] + residual, 64 tokens", 64, 1024, 2048, kernels.EPI_RESIDUAL),
+                  ("gate_up [6144x1024] + norm + silu*up, 64 tokens", 64, 6144, 1024, kernels.EPI_SILU_MUL),
+                  ("down [1024x3072] + residual, 64 tokens", 64, 1024, 3072, kernels.EPI_RESIDUAL)]
+        for name, m, n, k, epi in shapes:
+            copies = max(8, -(-(300 << 20) // (n * k)))
+            ws = torch.randint(-127, 128, (copies, n, k), dtype=torch.int8, device=dev, generator=g)
+            sc = (torch.rand(copies, n, device=dev, generator=g) * 0.001).to(torch.bfloat16)
+            x = torch.randn(m, k, device=dev, generator=g).to(torch.bfloat16)
+            nw = torch.ones(k, dtype=torch.bfloat16, device=dev)
+            resid = torch.randn(m, n, device=dev, generator=g).to(torch.bfloat16)
+            y = torch.empty(m, n // 2 if epi == kernels.EPI_SILU_MUL else n, dtype=torch.bfloat16, device=dev)
+            if epi == -1:
+                pos = torch.arange(m, device=dev) + 300
+                cos, sin = torch.randn(4096, 128, device=dev), torch.randn(4096, 128, device=dev)
+                slots = torch.arange(m, device=dev)
+                kc = torch.zeros(m, 8, 128, dtype=torch.bfloat16, device=dev)
+                vc = torch.zeros_like(kc)
 
+                def run(i):
+                    kernels.qkv_rope_cache_rows(x, ws[i], sc[i], 16, 8, 128, nw[:128], nw[:128], 1e-6, pos, cos, sin,
+                                                slots, kc, vc, norm_w=nw, eps=1e-6)
+            elif epi == kernels.EPI_SILU_MUL:
+                def run(i):
+                    kernels.int8_linear_rows(x, ws[i], sc[i], epi, norm_w=nw, eps=1e-6, out=y)
+            elif epi == kernels.EPI_RESIDUAL:
+                def run(i):
+                    kernels.int8_linear_rows(x, ws[i], sc[i], epi, residual=resid, out=y)
+            else:
+                def run(i):
+                    kernels.int8_linear_rows(x, ws[i], sc[i], out=y)
+            secs = hip_time(run, copies)
+            nbytes = linear_bytes(m, n, k)
+            print(json.dumps({"linear": name, "us_per_launch": round(secs * 1e6, 3), "bytes_per_launch": nbytes,
+                              "GB_s": round(nbytes / secs / 1e9, 1), "copies": copies}), flush=True)
+            del ws, sc
+        return 0
     cfg = workloads.QWEN3_0_6B
     batch = workloads.decode_batch(BATCH, CTX_LO, CTX_HI, seed=seed + 1, vocab=cfg["vocab_size"], spare_blocks=64)
-
     runner = ModelRunner.__new__(ModelRunner)
     runner.device, runner.block_size = dev, 16
     kv = torch.empty(cfg["num_hidden_layers"], 2, batch.num_blocks * 16, cfg["num_key_value_heads"], cfg["head_dim"],
                      dtype=torch.bfloat16, device=dev)
     workloads.fill_kv_pool_(kv, seed=seed + 2, on_device=True)
     runner.kv_caches = [(kv[i, 0], kv[i, 1]) for i in range(kv.shape[0])]
-    sched = [ScheduledChunk([0] * c, c - 1, 1, t) for c, t in zip(batch.context_lens, batch.block_tables, strict=True)]
-    secs, nbytes = time_attention(runner, sched, cfg)
-    print(json.dumps({"kernel": "paged_decode_kernel", "us_per_launch": secs * 1e6, "bytes_per_launch": nbytes,
+    sched = decode_sched(cfg, batch, seed + 3)
+    secs, nbytes, kname = time_layer_attention(runner, sched, cfg)
+    print(json.dumps({"kernel": kname, "us_per_launch": secs * 1e6, "bytes_per_launch": nbytes,
                       "GB_s": nbytes / secs / 1e9}))
     return 0
+
+
+WORKLOADS = {"decode": bench_decode, "linear": bench_linear, "attention": bench_attention, "prefill": bench_prefill,
+             "decode8b": bench_decode8b}
 
 
 def main() -> int:
@@ -189,143 +578,16 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--kernel-only", choices=["attention", "linear", "copy"], help="profiling entry point (see kernel_only)")
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="decode")
+    ap.add_argument("--kernel-only", choices=["attention", "linear", "copy"], help="profiling entry point")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
         return 2
     if args.kernel_only:
         return kernel_only(args.kernel_only, args.seed)
-
-    import torch
-
-    from miniserve_amd import kernels, workloads
-    from miniserve_amd.quant.int8 import quantize_int8_
-    from miniserve_amd.runner.model_runner import ModelRunner, ScheduledChunk
-    from miniserve_amd.runner.sampler import sample
-
-    dev = torch.device("cuda:0")
-    cfg = workloads.QWEN3_0_6B
-    t0 = time.time()
-    weights = workloads.random_weights(cfg, seed=args.seed)
-    model = workloads.build_model(cfg, weights, dev, max_positions=4096)
-    quantize_int8_(model)
-    batch = workloads.decode_batch(BATCH, CTX_LO, CTX_HI, seed=args.seed + 1, vocab=cfg["vocab_size"], spare_blocks=64)
-    runner = ModelRunner(model, dev, use_graphs=True, max_model_len=4096)
-    runner.allocate_kv_cache(batch.num_blocks)
-    workloads.fill_kv_pool_(runner.kv_cache, seed=args.seed + 2, on_device=True)
-    rng = random.Random(args.seed + 3)
-    sched = []
-    for c, table, tok in zip(batch.context_lens, batch.block_tables, batch.token_ids, strict=True):
-        sched.append(ScheduledChunk([rng.randrange(cfg["vocab_size"]) for _ in range(c - 1)] + [tok], c - 1, 1, table))
-    torch.cuda.synchronize()
-    print(f"[bench] setup {time.time() - t0:.1f}s: 28-layer int8 model, {batch.num_blocks} KV blocks", file=sys.stderr)
-
-    def eager_step() -> list[int]:
-        return sample(runner.forward_logits(runner.prepare(sched))).tolist()
-
-    def timed(fn, steps: int, warmup: int) -> float:
-        for _ in range(warmup):
-            fn()
-        torch.cuda.synchronize()
-        t = time.perf_counter()
-        for _ in range(steps):
-            fn()
-        torch.cuda.synchronize()
-        return (time.perf_counter() - t) / steps
-
-    eager_dt = timed(eager_step, max(3, args.steps // 4), 2)
-    graph_ids = runner.execute(sched)
-    if [g[0] for g in graph_ids] != eager_step():
-        raise RuntimeError("captured decode step disagrees with the eager step")
-    dt = timed(lambda: runner.execute(sched), args.steps, args.warmup)
-    tok_s = BATCH / dt
-    print(f"[bench] eager {eager_dt * 1e3:.3f} ms/step; graph {args.steps} steps: {dt * 1e3:.3f} ms/step, "
-          f"{tok_s:.0f} tok/s", file=sys.stderr)
-
-    attn_s, attn_b = time_attention(runner, sched, cfg)
-    achieved = attn_b / attn_s / 1e9
-    print(f"[bench] decode attention: {attn_s * 1e6:.2f} us/launch, {achieved:.0f} GB/s", file=sys.stderr)
-
-    result = {
-        "metric": METRIC,
-        "value": round(tok_s, 1),
-        "unit": "tok/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(dt * 1e3, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic",
-        "config": {
-            "workload": "Qwen3-0.6B-architecture int8 decode step (28 layers, random init)",
-            "batch": BATCH,
-            "context": f"{CTX_LO}+U[0,{CTX_HI - CTX_LO}]",
-            "sum_context": sum(batch.context_lens),
-            "kv_block": 16,
-            "weights": "int8 per-output-channel, bf16 activations, fp32 accumulation, tied bf16 LM head",
-            "parallelism": "none",
-            "hip_graph": True,
-            "eager_ms_per_step": round(eager_dt * 1e3, 4),
-        },
-        "roofline": {
-            "kernel": "paged_decode_kernel<2, 8>",
-            "bound": "hbm",
-            "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "bytes_per_launch": attn_b,
-            "us_per_launch": round(attn_s * 1e6, 3),
-        },
-    }
-
-    if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(cfg, weights, runner, sched)
-    print(json.dumps(result))
+    print(json.dumps(WORKLOADS[args.workload](args)))
     return 0
-
-
-def cpu_baseline(cfg, weights, runner, sched) -> dict:
-    """The CPU oracle's decode step on this host (same weights, same KV contents, same batch)."""
-    import platform
-
-    import torch
-
-    from oracle import model as om
-
-    cores = min(len(os.sched_getaffinity(0)), 16)
-    torch.set_num_threads(cores)
-    ocfg = om.Config.from_dict(cfg)
-    ow = om.quantize_weights(weights, ocfg)
-    okv = [(kc.cpu(), vc.cpu()) for kc, vc in runner.kv_caches]
-    tables = om.tables_for(ocfg, 4096)
-    step = om.prepare([(s.token_ids, s.num_computed, s.num_new, s.block_table) for s in sched], 16)
-    t = time.perf_counter()
-    om.run_step(ocfg, ow, okv, step, 16, tables)  # warm-up
-    first = time.perf_counter() - t
-    reps = max(1, min(5, int(20.0 / max(first, 1e-3))))
-    times = []
-    for _ in range(reps):
-        t = time.perf_counter()
-        om.run_step(ocfg, ow, okv, step, 16, tables)
-        times.append(time.perf_counter() - t)
-    times.sort()
-    med = times[len(times) // 2]
-    print(f"[bench] cpu oracle: {med:.3f} s/step on {cores} threads", file=sys.stderr)
-    return {
-        "value": round(BATCH / med, 2),
-        "unit": "tok/s",
-        "cores": cores,
-        "kind": "port",
-        "sample": f"the full decode step (64 tokens, 28 layers, LM head, argmax), median of {reps} after 1 warm-up",
-        "cpu": platform.processor() or platform.machine(),
-        "torch": torch.__version__,
-    }
 
 
 if __name__ == "__main__":

@@ -268,10 +268,18 @@ constexpr int64_t kGemmMinRows = 128;
 extern "C" int msa_int8_gemm(const uint16_t* x, int64_t m, int64_t k, int64_t ldx, const int8_t* qweight,
                              const uint16_t* scale, int64_t n, uint16_t* y, int64_t ldy, int epilogue,
                              const uint16_t* residual, int64_t ldr, msa_stream_t stream);
+extern "C" int msa_int8_linear_rows(const uint16_t* x, int64_t ldx, int64_t m, int64_t k, const uint16_t* norm_w,
+                                    float eps, const int8_t* qweight, const uint16_t* scale, int64_t n, int epilogue,
+                                    uint16_t* y, int64_t ldy, const uint16_t* residual, int64_t ldr,
+                                    msa_stream_t stream);
+
+// Smaller batches whose activation tile fits in LDS go to the token-split kernels (gemv_rows.hip).
+static bool rows_fits(int64_t k) { return k % 64 == 0 && 16 * (k + 8) * 2 + 16 * 1024 <= 160 * 1024; }
 
 extern "C" size_t msa_int8_linear_workspace_size(int64_t m, int64_t n, int64_t k) {
   if (m <= 0 || n <= 0 || k <= 0) return 0;
   if (m >= kGemmMinRows && k % 64 == 0) return 0;
+  if (rows_fits(k)) return 0;
   size_t best = 0;
   for (int epi = 0; epi < 3; ++epi) {
     const msa::SkinnyPlan p = msa::plan_skinny(m, n, k, epi, 0);
@@ -298,6 +306,8 @@ extern "C" int msa_int8_linear(const uint16_t* x, int64_t m, int64_t k, int64_t 
     return fail(MSA_ERR_INVALID, "msa_int8_linear: residual epilogue needs residual with ldr >= n");
   if (m >= kGemmMinRows && k % 64 == 0)
     return msa_int8_gemm(x, m, k, ldx, qweight, scale, n, y, ldy, epilogue, residual, ldr, stream);
+  if (rows_fits(k))
+    return msa_int8_linear_rows(x, ldx, m, k, nullptr, 0.f, qweight, scale, n, epilogue, y, ldy, residual, ldr, stream);
 
   SkinnyPlan p = plan_skinny(m, n, k, epilogue, 0);
   const size_t need = p.k_split > 1 ? (size_t)p.k_split * m * n * sizeof(float) : 0;
