@@ -120,14 +120,46 @@ __device__ __forceinline__ void block_to_tile(const RowsArgs& a, int& rb, int& m
   mc = slot % a.n_mc;
 }
 
-// Stage the tile's 16 activation rows in LDS (rows past the chunk repeat its last token), with the
-// prologue applied. NTH threads; TPT = NTH / 16 threads per row. Loads go out XB 16-byte vectors
-// per thread at a time and are waited for together: one memory round trip per XB vectors (for the
-// decode shapes, one in all), with the norm weights fetched alongside the first batch.
-template <int NTH, int PRO>
-__device__ __forceinline__ void stage_x(const RowsArgs& a, uint16_t* xs, int t0, int tcount, bool write_copy) {
-  constexpr int TPT = NTH / kTileTok;
-  constexpr int XB = 8;
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+// Stage the tile's ROWS activation rows in LDS (rows past the chunk repeat its last token), with the
+// prologue applied. NTH threads; TPT = NTH / ROWS threads per row. Two halves so the caller can
+// put other loads between them: stage_x_issue starts the first XB 16-byte vectors of each thread
+// (and the matching norm weights), stage_x_finish consumes them -- writing LDS, the RMSNorm -- and
+// loads any further vectors itself. The sum of squares runs on bf16 pairs (v_dot2_f32_bf16: exact
+// squares, float32 sums).
+constexpr int kStageXB = 8;
+
+template <int NTH, int PRO, int ROWS>
+__device__ __forceinline__ void stage_x_issue(const RowsArgs& a, int t0, int tcount, uint4 (&u)[kStageXB],
+                                              uint4 (&nw)[kStageXB]) {
+  constexpr int TPT = NTH / ROWS;
+  constexpr bool NORM = PRO == RB_PRO_RMSNORM || PRO == RB_PRO_GATHER_RMSNORM;
+  const int tl = threadIdx.x / TPT, q = threadIdx.x % TPT;
+  const int tok = t0 + (tl < tcount ? tl : tcount - 1);
+  int64_t src_row = tok;
+  if constexpr (PRO == RB_PRO_GATHER_RMSNORM || PRO == RB_PRO_GATHER) {
+    src_row = a.gather[tok];
+    src_row = src_row < 0 ? 0 : (src_row >= a.x_rows ? a.x_rows - 1 : src_row);  // memory safety only
+  }
+  const uint16_t* src = a.x + src_row * a.ldx;
+  const int nvec = a.k / 8;
+#pragma unroll
+  for (int b = 0; b < kStageXB; ++b) {
+    const int v = q + b * TPT;
+    u[b] = v < nvec ? *(const uint4*)(src + v * 8) : uint4{0, 0, 0, 0};
+    if constexpr (NORM) nw[b] = v < nvec ? *(const uint4*)(a.norm_w + v * 8) : uint4{0, 0, 0, 0};
+  }
+}
+
+template <int NTH, int PRO, int ROWS>
+__device__ __forceinline__ void stage_x_finish(const RowsArgs& a, uint16_t* xs, int t0, int tcount, bool write_copy,
+                                               uint4 (&u0)[kStageXB], const uint4 (&nw0)[kStageXB]) {
+  constexpr int TPT = NTH / ROWS;
+  constexpr int XB = kStageXB;
   constexpr bool NORM = PRO == RB_PRO_RMSNORM || PRO == RB_PRO_GATHER_RMSNORM;
   const int ldsx = a.k + 8;
   const int tl = threadIdx.x / TPT, q = threadIdx.x % TPT;
@@ -141,17 +173,13 @@ __device__ __forceinline__ void stage_x(const RowsArgs& a, uint16_t* xs, int t0,
   uint16_t* dst = xs + tl * ldsx;
   const int nvec = a.k / 8;
   const bool copy = NORM && write_copy && a.x_copy != nullptr && tl < tcount;
-  uint4 nw0[NORM ? XB : 1];
   float ss = 0.f;
   for (int v0 = q; v0 < nvec; v0 += XB * TPT) {
     uint4 u[XB];
 #pragma unroll
     for (int b = 0; b < XB; ++b) {
       const int v = v0 + b * TPT;
-      u[b] = v < nvec ? *(const uint4*)(src + v * 8) : uint4{0, 0, 0, 0};
-      if constexpr (NORM) {
-        if (v0 == q) nw0[b] = v < nvec ? *(const uint4*)(a.norm_w + v * 8) : uint4{0, 0, 0, 0};
-      }
+      u[b] = v0 == q ? u0[b] : (v < nvec ? *(const uint4*)(src + v * 8) : uint4{0, 0, 0, 0});
     }
 #pragma unroll
     for (int b = 0; b < XB; ++b) {
@@ -160,12 +188,10 @@ __device__ __forceinline__ void stage_x(const RowsArgs& a, uint16_t* xs, int t0,
         *(uint4*)(dst + v * 8) = u[b];
         if constexpr (NORM) {
           if (copy) *(uint4*)(a.x_copy + (int64_t)tok * a.ld_copy + v * 8) = u[b];
-          const uint32_t e[4] = {u[b].x, u[b].y, u[b].z, u[b].w};
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float lo = bf16lo(e[i]), hi = bf16hi(e[i]);
-            ss += lo * lo + hi * hi;
-          }
+          ss = dot2_bf16(u[b].x, u[b].x, ss);
+          ss = dot2_bf16(u[b].y, u[b].y, ss);
+          ss = dot2_bf16(u[b].z, u[b].z, ss);
+          ss = dot2_bf16(u[b].w, u[b].w, ss);
         }
       }
     }
@@ -184,8 +210,8 @@ __device__ __forceinline__ void stage_x(const RowsArgs& a, uint16_t* xs, int t0,
       for (int b = 0; b < XB; ++b) {
         const int v = v0 + b * TPT;
         if (v < nvec) {
-          const uint4 u = *(const uint4*)(dst + v * 8);  // this thread's own LDS stores above
-          const uint32_t e[4] = {u.x, u.y, u.z, u.w}, ww[4] = {wv[b].x, wv[b].y, wv[b].z, wv[b].w};
+          const uint4 uu = *(const uint4*)(dst + v * 8);  // this thread's own LDS stores above
+          const uint32_t e[4] = {uu.x, uu.y, uu.z, uu.w}, ww[4] = {wv[b].x, wv[b].y, wv[b].z, wv[b].w};
           uint32_t o[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
@@ -199,6 +225,13 @@ __device__ __forceinline__ void stage_x(const RowsArgs& a, uint16_t* xs, int t0,
   }
 }
 
+template <int NTH, int PRO, int ROWS = kTileTok>
+__device__ __forceinline__ void stage_x(const RowsArgs& a, uint16_t* xs, int t0, int tcount, bool write_copy) {
+  uint4 u[kStageXB], nw[kStageXB];
+  stage_x_issue<NTH, PRO, ROWS>(a, t0, tcount, u, nw);
+  stage_x_finish<NTH, PRO, ROWS>(a, xs, t0, tcount, write_copy, u, nw);
+}
+
 // Weight row of (row block rb, row tile rt, sub-tile nt, lane row j).
 template <int RT, int NTW, int EPI>
 __device__ __forceinline__ int rows_row(const RowsArgs& a, int rb, int rt, int nt, int j) {
@@ -209,14 +242,55 @@ __device__ __forceinline__ int rows_row(const RowsArgs& a, int rb, int rt, int n
   }
 }
 
-// The qkv epilogue: ot holds bf16-rounded outputs [16 tokens][128 + 4] of head slot hs (q heads,
-// then k heads, then v heads). q/k: per-head RMSNorm then RoPE with pairs (i, i + 64), rounding as
-// model/layers.py:18-22 and :61-65; v: copied. Keys and values go to the cache slot of their token.
-template <int NTH>
-__device__ __forceinline__ void qkv_head_epilogue(const RowsArgs& a, const float* ot, int hs, int t0, int tcount) {
+// The qkv epilogue: ot holds bf16-rounded outputs [ROWS tokens][128 + 4] of head slot hs (q
+// heads, then k heads, then v heads). q/k: per-head RMSNorm then RoPE with pairs (i, i + 64),
+// rounding as model/layers.py:18-22 and :61-65; v: copied. Keys and values go to the cache slot of
+// their token. Thread (tl, q) handles token tl, dims q + p * TPT (and + 64) for p < PPT; its
+// position / slot and its cos / sin / norm weights are loaded by qkv_epi_prefetch* ahead of time.
+template <int NTH, int ROWS>
+struct QkvEpi {
+  static constexpr int TPT = NTH / ROWS;
+  static constexpr int PPT = 64 / TPT;
+  int64_t pos, slot;
+  float c0[PPT], c1[PPT], s0[PPT], s1[PPT], w0[PPT], w1[PPT];
+};
+
+template <int NTH, int ROWS>
+__device__ __forceinline__ void qkv_epi_prefetch_pos(const RowsArgs& a, int hs, int t0, int tcount, QkvEpi<NTH, ROWS>& e) {
+  constexpr int TPT = QkvEpi<NTH, ROWS>::TPT;
+  const int tl = threadIdx.x / TPT;
+  const int tok = t0 + (tl < tcount ? tl : tcount - 1);
+  e.pos = hs < a.heads + a.kv_heads ? a.positions[tok] : 0;  // v heads need no position
+  e.slot = hs >= a.heads ? a.slots[tok] : 0;                 // q heads need no slot
+}
+
+template <int NTH, int ROWS>
+__device__ __forceinline__ void qkv_epi_prefetch_tables(const RowsArgs& a, int hs, QkvEpi<NTH, ROWS>& e) {
+  constexpr int TPT = QkvEpi<NTH, ROWS>::TPT, PPT = QkvEpi<NTH, ROWS>::PPT;
+  if (hs >= a.heads + a.kv_heads) return;  // v heads: copied as they are
+  const int q = threadIdx.x % TPT;
+  const int64_t pos = e.pos < 0 ? 0 : (e.pos >= a.max_pos ? a.max_pos - 1 : e.pos);  // memory safety only
+  const float* cr = a.cos_t + pos * 128;
+  const float* sr = a.sin_t + pos * 128;
+  const uint16_t* nw = hs < a.heads ? a.qn_w : a.kn_w;
+#pragma unroll
+  for (int p = 0; p < PPT; ++p) {
+    const int i = q + p * TPT;
+    e.c0[p] = cr[i];
+    e.c1[p] = cr[i + 64];
+    e.s0[p] = sr[i];
+    e.s1[p] = sr[i + 64];
+    e.w0[p] = bf16_to_f32(nw[i]);
+    e.w1[p] = bf16_to_f32(nw[i + 64]);
+  }
+}
+
+template <int NTH, int ROWS>
+__device__ __forceinline__ void qkv_head_epilogue(const RowsArgs& a, const float* ot, int hs, int t0, int tcount,
+                                                  const QkvEpi<NTH, ROWS>& e) {
   constexpr int D = 128, HALF = 64, OTS = D + 4;
-  constexpr int TPT = NTH / kTileTok;  // threads per token
-  constexpr int PPT = HALF / TPT;      // rotary pairs per thread
+  constexpr int TPT = QkvEpi<NTH, ROWS>::TPT;  // threads per token
+  constexpr int PPT = QkvEpi<NTH, ROWS>::PPT;  // rotary pairs per thread
   const int tl = threadIdx.x / TPT, q = threadIdx.x % TPT;
   if (tl >= tcount) return;  // whole groups leave together; no barrier follows
   const int tok = t0 + tl;
@@ -226,10 +300,9 @@ __device__ __forceinline__ void qkv_head_epilogue(const RowsArgs& a, const float
   if (is_q) {
     dst = a.q_out + ((int64_t)tok * a.heads + hs) * D;
   } else {
-    const int64_t slot = a.slots[tok];
-    if (slot < 0 || slot >= a.num_slots) return;
+    if (e.slot < 0 || e.slot >= a.num_slots) return;
     const int kvh = is_v ? hs - a.heads - a.kv_heads : hs - a.heads;
-    dst = (is_v ? a.vc : a.kc) + (slot * a.kv_heads + kvh) * D;
+    dst = (is_v ? a.vc : a.kc) + (e.slot * a.kv_heads + kvh) * D;
   }
   if (is_v) {
 #pragma unroll
@@ -250,30 +323,27 @@ __device__ __forceinline__ void qkv_head_epilogue(const RowsArgs& a, const float
   }
   ss = group_sum<TPT>(ss);
   const float r = 1.0f / sqrtf(ss / (float)D + a.head_eps);
-  const uint16_t* nw = is_q ? a.qn_w : a.kn_w;
-  int64_t pos = a.positions[tok];
-  pos = pos < 0 ? 0 : (pos >= a.max_pos ? a.max_pos - 1 : pos);  // memory safety only
-  const float* cr = a.cos_t + pos * D;
-  const float* sr = a.sin_t + pos * D;
 #pragma unroll
   for (int p = 0; p < PPT; ++p) {
     const int i = q + p * TPT;
-    const float x0 = round_bf16(bf16_to_f32(nw[i]) * round_bf16(lo[p] * r));
-    const float x1 = round_bf16(bf16_to_f32(nw[i + HALF]) * round_bf16(hi[p] * r));
-    const float c0 = round_bf16(cr[i]), c1 = round_bf16(cr[i + HALF]);
-    const float s0 = round_bf16(sr[i]), s1 = round_bf16(sr[i + HALF]);
+    const float x0 = round_bf16(e.w0[p] * round_bf16(lo[p] * r));
+    const float x1 = round_bf16(e.w1[p] * round_bf16(hi[p] * r));
+    const float c0 = round_bf16(e.c0[p]), c1 = round_bf16(e.c1[p]);
+    const float s0 = round_bf16(e.s0[p]), s1 = round_bf16(e.s1[p]);
     dst[i] = f32_to_bf16(round_bf16(x0 * c0) + round_bf16(-x1 * s0));
     dst[i + HALF] = f32_to_bf16(round_bf16(x1 * c1) + round_bf16(x0 * s1));
   }
 }
 
 // int8 weights. RT row tiles (x NTW sub-tiles of 16 rows) per workgroup, each row tile's K split
-// over KW wavefronts; CPW = 64-wide K chunks a wavefront holds in registers at once.
-template <int RT, int NTW, int KW, int CPW, int PRO, int EPI>
+// over KW wavefronts; CPW = 64-wide K chunks a wavefront holds in registers at once; MT 16-token
+// MFMA tiles per workgroup (each dequantized weight fragment feeds MT MFMAs).
+template <int RT, int NTW, int KW, int CPW, int PRO, int EPI, int MT = 1>
 __global__ __launch_bounds__(64 * RT * KW) void int8_rows_kernel(RowsArgs a) {
   constexpr int NTH = 64 * RT * KW;
+  constexpr int ROWS = 16 * MT;
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
-  uint16_t* xs = smem;  // [16][k + 8]
+  uint16_t* xs = smem;  // [ROWS][k + 8]
   const int ldsx = a.k + 8;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j = lane & 15, g = lane >> 4;
@@ -305,13 +375,40 @@ __global__ __launch_bounds__(64 * RT * KW) void int8_rows_kernel(RowsArgs a) {
       for (int nt = 0; nt < NTW; ++nt)
         wv[c][nt] = c0 + c < c_end ? *(const uint4*)(wp[nt] + (int64_t)(c0 + c) * kRowsChunk) : uint4{0, 0, 0, 0};
   };
+  // Issue order = completion order: activations (and norm weights), then the epilogue's inputs,
+  // then the weights -- so the prologue runs while the weights are still in flight.
+  uint4 xu[kStageXB], xnw[kStageXB];
+  stage_x_issue<NTH, PRO, ROWS>(a, t0, tcount, xu, xnw);
+  uint16_t rpre[MT][NTW][4];  // residual values of this lane's outputs
+  if constexpr (EPI == RB_EPI_RESIDUAL) {
+    if (ks == 0) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NTW; ++nt) {
+          int row = rows_row<RT, NTW, EPI>(a, rb, rt, nt, j);
+          row = row < a.n ? row : a.n - 1;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int tl = mt * 16 + 4 * g + i;
+            const int64_t tok = t0 + (tl < tcount ? tl : tcount - 1);
+            rpre[mt][nt][i] = a.resid[tok * a.ldr + row];
+          }
+        }
+    }
+  }
+  QkvEpi<NTH, ROWS> qe;
+  if constexpr (EPI == RB_EPI_QKV) qkv_epi_prefetch_pos<NTH, ROWS>(a, rb, t0, tcount, qe);
   load_batch(c_begin);
-  stage_x<NTH, PRO>(a, xs, t0, tcount, rb == 0);
+  stage_x_finish<NTH, PRO, ROWS>(a, xs, t0, tcount, rb == 0, xu, xnw);
+  if constexpr (EPI == RB_EPI_QKV) qkv_epi_prefetch_tables<NTH, ROWS>(a, rb, qe);
   __syncthreads();
 
-  f32x4 acc[NTW];
+  f32x4 acc[MT][NTW];
 #pragma unroll
-  for (int nt = 0; nt < NTW; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NTW; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
   const uint16_t* xrow = xs + j * ldsx + g * 16;
   for (int c0 = c_begin; c0 < c_end; c0 += CPW) {
     if (c0 != c_begin) load_batch(c0);
@@ -320,12 +417,17 @@ __global__ __launch_bounds__(64 * RT * KW) void int8_rows_kernel(RowsArgs a) {
       if (c0 + c < c_end) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          const bf16x8 av = *(const bf16x8*)(xrow + (c0 + c) * kRowsChunk + h * 8);
+          bf16x8 av[MT];
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+            av[mt] = *(const bf16x8*)(xrow + mt * 16 * ldsx + (c0 + c) * kRowsChunk + h * 8);
 #pragma unroll
           for (int nt = 0; nt < NTW; ++nt) {
             const bf16x8 bv = h == 0 ? dequant8_rows(wv[c][nt].x, wv[c][nt].y, sc[nt])
                                      : dequant8_rows(wv[c][nt].z, wv[c][nt].w, sc[nt]);
-            acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, acc[nt], 0, 0, 0);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+              acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[mt], bv, acc[mt][nt], 0, 0, 0);
           }
         }
       }
@@ -333,49 +435,57 @@ __global__ __launch_bounds__(64 * RT * KW) void int8_rows_kernel(RowsArgs a) {
   }
 
   if constexpr (KW > 1) {
-    f32x4* red = (f32x4*)(smem + kTileTok * ldsx);  // [KW - 1][RT][NTW][64]
+    f32x4* red = (f32x4*)(smem + ROWS * ldsx);  // [KW - 1][RT][NTW][MT][64]
     if (ks > 0) {
 #pragma unroll
-      for (int nt = 0; nt < NTW; ++nt) red[(((ks - 1) * RT + rt) * NTW + nt) * 64 + lane] = acc[nt];
+      for (int nt = 0; nt < NTW; ++nt)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) red[((((ks - 1) * RT + rt) * NTW + nt) * MT + mt) * 64 + lane] = acc[mt][nt];
     }
     __syncthreads();
     if (ks == 0) {
       for (int s = 1; s < KW; ++s)
 #pragma unroll
-        for (int nt = 0; nt < NTW; ++nt) acc[nt] += red[(((s - 1) * RT + rt) * NTW + nt) * 64 + lane];
+        for (int nt = 0; nt < NTW; ++nt)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) acc[mt][nt] += red[((((s - 1) * RT + rt) * NTW + nt) * MT + mt) * 64 + lane];
     }
   }
 
   if constexpr (EPI == RB_EPI_QKV) {
-    float* ot = (float*)(smem + kTileTok * ldsx) + (KW > 1 ? (KW - 1) * RT * NTW * 256 : 0);  // [16][132]
+    float* ot = (float*)(smem + ROWS * ldsx) + (KW > 1 ? (KW - 1) * RT * NTW * MT * 256 : 0);  // [ROWS][132]
     if (ks == 0) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) ot[(4 * g + i) * 132 + rt * 16 + j] = round_bf16(acc[0][i]);
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ot[(mt * 16 + 4 * g + i) * 132 + rt * 16 + j] = round_bf16(acc[mt][0][i]);
     }
     __syncthreads();
-    qkv_head_epilogue<NTH>(a, ot, rb, t0, tcount);
+    qkv_head_epilogue<NTH, ROWS>(a, ot, rb, t0, tcount, qe);
     return;
   } else {
     if (ks != 0) return;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int tl = 4 * g + i;
-      if (tl >= tcount) continue;
-      const int64_t tok = t0 + tl;
-      if constexpr (EPI == RB_EPI_SILU_MUL) {
-        const int col = rb * (RT * 16) + rt * 16 + j;
-        if (col < a.n / 2) a.y[tok * a.ldy + col] = f32_to_bf16(silu_mul_rows(acc[0][i], acc[1][i]));
-      } else {
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int nt = 0; nt < NTW; ++nt) {
-          const int row = rows_row<RT, NTW, EPI>(a, rb, rt, nt, j);
-          if (row >= a.n) continue;
-          float v = round_bf16(acc[nt][i]);
-          if constexpr (EPI == RB_EPI_RESIDUAL) v += bf16_to_f32(a.resid[tok * a.ldr + row]);
-          a.y[tok * a.ldy + row] = f32_to_bf16(v);
+      for (int i = 0; i < 4; ++i) {
+        const int tl = mt * 16 + 4 * g + i;
+        if (tl >= tcount) continue;
+        const int64_t tok = t0 + tl;
+        if constexpr (EPI == RB_EPI_SILU_MUL) {
+          const int col = rb * (RT * 16) + rt * 16 + j;
+          if (col < a.n / 2) a.y[tok * a.ldy + col] = f32_to_bf16(silu_mul_rows(acc[mt][0][i], acc[mt][1][i]));
+        } else {
+#pragma unroll
+          for (int nt = 0; nt < NTW; ++nt) {
+            const int row = rows_row<RT, NTW, EPI>(a, rb, rt, nt, j);
+            if (row >= a.n) continue;
+            float v = round_bf16(acc[mt][nt][i]);
+            if constexpr (EPI == RB_EPI_RESIDUAL) v += bf16_to_f32(rpre[mt][nt][i]);
+            a.y[tok * a.ldy + row] = f32_to_bf16(v);
+          }
         }
       }
-    }
   }
 }
 
@@ -590,7 +700,18 @@ extern "C" int msa_int8_linear_rows(const uint16_t* x, int64_t ldx, int64_t m, i
   hipStream_t s = (hipStream_t)stream;
   const size_t xt = x_tile_bytes((int)k);
   int rc;
-  if (epilogue == MSA_EPI_SILU_MUL) {
+  if (epilogue == MSA_EPI_SILU_MUL && m > 16 && 2 * xt + 3 * 2 * 2 * 2 * 1024 <= kMaxLds) {
+    // 32 tokens x (32 gate + 32 up) rows per workgroup: 2 row tiles x (gate, up) x 4 K slices;
+    // each dequantized weight fragment feeds both 16-token MFMA tiles.
+    a.n_rb = (int)((n / 2 + 31) / 32);
+    a.tpw = 32;
+    a.n_mc = (int)((m + a.tpw - 1) / a.tpw);
+    const size_t lds = 2 * xt + 3 * 2 * 2 * 2 * 1024;
+    if (pro == RB_PRO_RMSNORM)
+      rc = launch_rows(int8_rows_kernel<2, 2, 4, 4, RB_PRO_RMSNORM, RB_EPI_SILU_MUL, 2>, 512, lds, grid_blocks(a), a, s);
+    else
+      rc = launch_rows(int8_rows_kernel<2, 2, 4, 4, RB_PRO_NONE, RB_EPI_SILU_MUL, 2>, 512, lds, grid_blocks(a), a, s);
+  } else if (epilogue == MSA_EPI_SILU_MUL) {
     // 64 gate + 64 up rows per workgroup: 4 row tiles x (gate, up) x 2 K slices.
     a.n_rb = (int)((n / 2 + 63) / 64);
     a.tpw = tokens_per_wg(m, a.n_rb);
