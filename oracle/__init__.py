@@ -23,6 +23,8 @@ How it is pinned (what a plausible mistake would trip):
 * ``attention`` -- float64 brute-force dense softmax attention per sequence through the block
   table, invariance under permuted physical block placement, and batched == alone.
 * ``model.greedy`` -- ``np.argmax`` (first index wins ties).
+* all of the above -- the golden fixtures of ``tests/golden/`` (numpy, float64 brute force and
+  transformers' float64 Qwen3; ``tests/test_golden.py``).
 
 Nothing here is "parity unpinned".
 """

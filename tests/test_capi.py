@@ -77,7 +77,9 @@ def test_zero_sized_calls_are_no_ops():
 
 def test_workspace_sizes():
     assert _native.query("msa_int8_linear_workspace_size", 1, 1024, 64) == 0  # one K chunk per wave: no split
-    assert _native.query("msa_int8_linear_workspace_size", 64, 1024, 2048) > 0
+    assert _native.query("msa_int8_linear_workspace_size", 64, 1024, 2048) == 0  # token-split kernel
+    assert _native.query("msa_int8_linear_workspace_size", 256, 1024, 2048) == 0  # LDS-tiled GEMM
+    assert _native.query("msa_int8_linear_workspace_size", 64, 1024, 2000) > 0  # K % 64 != 0: split-K
     assert _native.query("msa_paged_attention_decode_workspace_size", 64, 16, 128, 1) == 0
     ws = _native.query("msa_paged_attention_decode_workspace_size", 64, 16, 128, 8)
     assert ws >= 64 * 16 * 8 * (128 + 2) * 4
