@@ -2,8 +2,8 @@
 
 Every op launches on the current HIP stream of its tensors' device and never synchronizes. Bad
 arguments raise ``RuntimeError`` before anything is launched (the convention of a TORCH_CHECK).
-Workspaces are device scratch buffers owned here (one per kind and device, grown on demand and
-reserved before any graph capture); kernels never need them zeroed.
+Workspaces are device scratch buffers owned here (one per kind, device and stream, grown on
+demand and reserved before any graph capture); kernels never need them zeroed.
 """
 
 from __future__ import annotations
@@ -39,13 +39,16 @@ def _on_gpu(*ts: Tensor) -> None:
 
 
 class _Workspaces:
+    """Device scratch per (kind, device, stream): calls on one stream are ordered by it, so they
+    share a buffer; calls on different streams (concurrent graph branches) never do."""
+
     def __init__(self) -> None:
-        self._bufs: dict[tuple[str, int], Tensor] = {}
+        self._bufs: dict[tuple[str, int, int], Tensor] = {}
 
     def get(self, kind: str, device: torch.device, nbytes: int) -> Tensor | None:
         if nbytes == 0:
             return None
-        key = (kind, device.index or 0)
+        key = (kind, device.index or 0, torch.cuda.current_stream(device).cuda_stream)
         buf = self._bufs.get(key)
         if buf is None or buf.numel() < nbytes:
             _check(
