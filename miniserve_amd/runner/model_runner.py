@@ -71,14 +71,16 @@ class CapturedDecode:
         self.host_i64[2 * b : 3 * b] = -1  # warm-up rows write no KV slot (kernels skip slot < 0)
         self.dev.copy_(self.host)
         model = runner.model
-        stream = torch.cuda.Stream(device=dev)
+        # Warm-up and capture on one stream: workspaces are kept per stream, so the warm-up
+        # reserves exactly the buffers the captured kernels use.
+        self.stream = stream = torch.cuda.Stream(device=dev)
         stream.wait_stream(torch.cuda.current_stream(dev))
         with torch.cuda.stream(stream), torch.inference_mode():
-            for _ in range(2):  # warm-up: reserves every workspace before capture
+            for _ in range(2):
                 model.greedy(self.ids, self.pos, runner.kv_caches, self.meta, self.rows)
         torch.cuda.current_stream(dev).wait_stream(stream)
         self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph), torch.inference_mode():
+        with torch.cuda.graph(self.graph, stream=stream), torch.inference_mode():
             self.out_ids = model.greedy(self.ids, self.pos, runner.kv_caches, self.meta, self.rows)
 
     def run(self, scheduled: list[ScheduledChunk], block_size: int) -> list[int]:
