@@ -496,17 +496,40 @@ __global__ __launch_bounds__(64 * RT * KW) void int8_rows_kernel(RowsArgs a) {
 // flight), multiplies on MFMA against the MT token tiles, rounds each logit to bf16 (the
 // reference's logits dtype) and keeps a running (max, first index) per token. The waves then meet
 // in LDS and write one candidate per (workgroup, token); argmax_candidates_kernel picks the winner.
-template <int W, int MT, int PRO>
+template <int W, int MT, int PRO, int PF>
 __global__ __launch_bounds__(64 * W) void lm_head_argmax_kernel(RowsArgs a) {
   constexpr int CH = 32;  // K per chunk (bf16: 16 bytes per lane)
-  constexpr int PF = 8;   // chunks in flight per wave
   constexpr int NTH = 64 * W;
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
   const int ldsx = a.k + 8;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j = lane & 15, g = lane >> 4;
 
-  // Stage the (up to 64) rows: 16-row tiles, each with the RMSNorm prologue.
+  const int ntiles = (a.n + 15) / 16;
+  const int nch = a.k / CH;  // a multiple of PF (the host picks PF)
+  const int stride = gridDim.x * W;
+  const int first = blockIdx.x * W + wave;
+  // The load cursor runs PF chunks ahead of the MFMAs across tile boundaries (the wave's tiles are
+  // first, first + stride, ...), so the ring never drains between tiles; chunk c of every tile
+  // lands in ring slot c % PF because PF divides the chunks per tile.
+  auto row_ptr = [&](int tile) {
+    const int row = tile * 16 + j;
+    return (const uint16_t*)a.w + (int64_t)(row < a.n ? row : a.n - 1) * a.k + g * 8;
+  };
+  int ld_tile = first, ld_c = 0;
+  const uint16_t* ld_p = row_ptr(ld_tile);
+  uint4 wv[PF];
+#pragma unroll
+  for (int c = 0; c < PF; ++c) {
+    wv[c] = ld_tile < ntiles ? *(const uint4*)(ld_p + ld_c * CH) : uint4{0, 0, 0, 0};
+    if (++ld_c == nch) {
+      ld_c = 0;
+      ld_tile += stride;
+      ld_p = row_ptr(ld_tile);
+    }
+  }
+  // Stage the (up to 64) rows while the first weight chunks are in flight: 16-row tiles, each
+  // with the RMSNorm prologue.
   for (int mt = 0; mt < MT; ++mt) {
     const int t0 = mt * 16;
     const int tcount = max(1, min(16, a.t - t0));
@@ -523,28 +546,26 @@ __global__ __launch_bounds__(64 * W) void lm_head_argmax_kernel(RowsArgs a) {
       best[mt][i] = -INFINITY;
       bidx[mt][i] = 0x7fffffff;
     }
-  const int ntiles = (a.n + 15) / 16;
-  const int nch = a.k / CH;
-  for (int tile = blockIdx.x * W + wave; tile < ntiles; tile += gridDim.x * W) {
+
+  for (int tile = first; tile < ntiles; tile += stride) {
     const int row = tile * 16 + j;
-    const uint16_t* wp = (const uint16_t*)a.w + (int64_t)(row < a.n ? row : a.n - 1) * a.k + g * 8;
     f32x4 acc[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    uint4 wv[PF];
-#pragma unroll
-    for (int c = 0; c < PF; ++c) wv[c] = c < nch ? *(const uint4*)(wp + c * CH) : uint4{0, 0, 0, 0};
     for (int c0 = 0; c0 < nch; c0 += PF) {
 #pragma unroll
       for (int c = 0; c < PF; ++c) {
-        if (c0 + c < nch) {
-          const uint4 cur = wv[c];
-          if (c0 + c + PF < nch) wv[c] = *(const uint4*)(wp + (c0 + c + PF) * CH);
+        const uint4 cur = wv[c];
+        if (ld_tile < ntiles) wv[c] = *(const uint4*)(ld_p + ld_c * CH);  // wave-uniform
+        if (++ld_c == nch) {
+          ld_c = 0;
+          ld_tile += stride;
+          ld_p = row_ptr(ld_tile);
+        }
 #pragma unroll
-          for (int mt = 0; mt < MT; ++mt) {
-            const bf16x8 av = *(const bf16x8*)(smem + (mt * 16 + j) * ldsx + (c0 + c) * CH + g * 8);
-            acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8, cur), acc[mt], 0, 0, 0);
-          }
+        for (int mt = 0; mt < MT; ++mt) {
+          const bf16x8 av = *(const bf16x8*)(smem + (mt * 16 + j) * ldsx + (c0 + c) * CH + g * 8);
+          acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8, cur), acc[mt], 0, 0, 0);
         }
       }
     }
@@ -817,6 +838,7 @@ extern "C" int msa_lm_head_argmax(const uint16_t* hidden, int64_t ld_hidden, int
   if (!workspace || workspace_bytes < need) return fail(MSA_ERR_WORKSPACE, "msa_lm_head_argmax: workspace too small");
   if (!aligned16(workspace)) return fail(MSA_ERR_INVALID, "msa_lm_head_argmax: workspace must be 16-byte aligned");
   hipStream_t s = (hipStream_t)stream;
+  const int64_t nch = k / 32;  // 32-wide K chunks per vocabulary row; the load ring depth divides it
   float* cand_val = (float*)workspace;
   int32_t* cand_idx = (int32_t*)((char*)workspace + (size_t)num_rows * kLmBlocks * sizeof(float));
   // Launches of up to 64 rows each (fewer when 16-row activation tiles of this width fill LDS);
@@ -835,9 +857,13 @@ extern "C" int msa_lm_head_argmax(const uint16_t* hidden, int64_t ld_hidden, int
     a.cand_val = cand_val + r0 * kLmBlocks;
     a.cand_idx = cand_idx + r0 * kLmBlocks;
     int rc;
-#define MSA_LM_LAUNCH(MT)                                                                                        \
-  rc = norm_w ? launch_rows(lm_head_argmax_kernel<W, MT, RB_PRO_GATHER_RMSNORM>, 64 * W, lds, kLmBlocks, a, s) \
-              : launch_rows(lm_head_argmax_kernel<W, MT, RB_PRO_GATHER>, 64 * W, lds, kLmBlocks, a, s)
+#define MSA_LM_LAUNCH_PF(MT, PF)                                                                                     \
+  rc = norm_w ? launch_rows(lm_head_argmax_kernel<W, MT, RB_PRO_GATHER_RMSNORM, PF>, 64 * W, lds, kLmBlocks, a, s) \
+              : launch_rows(lm_head_argmax_kernel<W, MT, RB_PRO_GATHER, PF>, 64 * W, lds, kLmBlocks, a, s)
+#define MSA_LM_LAUNCH(MT)                                  \
+  if (nch % 16 == 0) MSA_LM_LAUNCH_PF(MT, 16);             \
+  else if (nch % 4 == 0) MSA_LM_LAUNCH_PF(MT, 4);          \
+  else MSA_LM_LAUNCH_PF(MT, 1);
     switch (mt) {
       case 1: MSA_LM_LAUNCH(1); break;
       case 2: MSA_LM_LAUNCH(2); break;
@@ -845,6 +871,7 @@ extern "C" int msa_lm_head_argmax(const uint16_t* hidden, int64_t ld_hidden, int
       default: MSA_LM_LAUNCH(4); break;
     }
 #undef MSA_LM_LAUNCH
+#undef MSA_LM_LAUNCH_PF
     if (rc != MSA_OK) return rc;
     rc = check_launch("msa_lm_head_argmax");
     if (rc != MSA_OK) return rc;
