@@ -113,8 +113,10 @@ int msa_qkv_rope_cache_rows(const uint16_t* x, int64_t ldx, int64_t x_rows, cons
                             int64_t max_positions, const int64_t* slot_mapping, uint16_t* q_out,
                             uint16_t* k_cache, uint16_t* v_cache, int64_t num_slots, msa_stream_t stream);
 
-/* Bytes of workspace msa_lm_head_argmax needs (per-row-block argmax candidates). */
-size_t msa_lm_head_argmax_workspace_size(int64_t num_rows, int64_t vocab);
+/* Bytes of workspace msa_lm_head_argmax needs for num_rows rows of width k over a vocabulary of
+ * vocab entries (per-block argmax candidates; with many rows at a large k also the normalized
+ * rows of the GEMM route). */
+size_t msa_lm_head_argmax_workspace_size(int64_t num_rows, int64_t k, int64_t vocab);
 
 /* Final norm + LM head + greedy sampling (model/qwen3.py:152-158, runner/model_runner.py:217,
  * runner/sampler.py:59) without materializing logits: for each i < num_rows,
@@ -122,7 +124,9 @@ size_t msa_lm_head_argmax_workspace_size(int64_t num_rows, int64_t vocab);
  * [0, hidden_rows)) with the first index winning
  * ties -- the argmax of the reference's bf16 logits cast to float32. norm_w NULL: the rows are
  * taken as already normalized. weight [vocab, k] bf16 (the tied embedding or the LM head).
- * k % 32 == 0. */
+ * k % 32 == 0. Up to 64 rows (fewer at large k) stream the weight once with the rows in LDS;
+ * more rows (k % 64 == 0) normalize into the workspace and run an MFMA GEMM whose tiles keep
+ * only each row's best entry. */
 int msa_lm_head_argmax(const uint16_t* hidden, int64_t ld_hidden, int64_t hidden_rows, const int64_t* rows,
                        int64_t num_rows, int64_t k,
                        const uint16_t* norm_w, float eps, const uint16_t* weight, int64_t vocab, int64_t* out_ids,

@@ -193,6 +193,226 @@ static int launch_gemm(const GemmArgs& a, int blocks, hipStream_t s) {
   return MSA_OK;
 }
 
+// ---- LM head for many rows: gather + RMSNorm once, then a bf16 GEMM with an argmax epilogue ----
+//
+// When the sampled rows do not fit one LDS activation tile of the streaming LM head (many rows at
+// a large hidden size), the rows are normalized once into a workspace and the logits are
+// computed tile by tile on MFMA: 128 rows x 128 vocabulary entries x 64-wide K steps, both
+// operands bf16 in LDS, double buffered. No logit leaves the workgroup: each one is rounded to
+// bf16 (the reference's logits dtype) and the workgroup writes one (max, first index) candidate
+// per row for its 128 vocabulary entries.
+
+// One workgroup per row: y[r] = bf16(w * bf16(x[rows[r]] * rsqrt(mean(x^2) + eps))), or the plain
+// gathered row when w is null. Squares are exact (bf16 pairs on v_dot2), sums float32.
+__global__ __launch_bounds__(256) void lm_rows_prologue_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                               int64_t x_rows, const int64_t* __restrict__ rows,
+                                                               const uint16_t* __restrict__ w, float eps, int k,
+                                                               uint16_t* __restrict__ y) {
+  __shared__ float red[4];
+  int64_t src = rows[blockIdx.x];
+  src = src < 0 ? 0 : (src >= x_rows ? x_rows - 1 : src);  // memory safety only
+  const uint16_t* xr = x + src * ldx;
+  uint16_t* yr = y + (int64_t)blockIdx.x * k;
+  const int nvec = k / 8;
+  if (!w) {
+    for (int v = threadIdx.x; v < nvec; v += 256) *(uint4*)(yr + v * 8) = *(const uint4*)(xr + v * 8);
+    return;
+  }
+  float ss = 0.f;
+  for (int v = threadIdx.x; v < nvec; v += 256) {
+    const uint4 u = *(const uint4*)(xr + v * 8);
+    ss = dot2_bf16(u.x, u.x, ss);
+    ss = dot2_bf16(u.y, u.y, ss);
+    ss = dot2_bf16(u.z, u.z, ss);
+    ss = dot2_bf16(u.w, u.w, ss);
+  }
+  ss = row16_sum(ss);
+  ss = xrow_sum(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  ss = red[0] + red[1] + red[2] + red[3];
+  const float r = 1.0f / sqrtf(ss / (float)k + eps);
+  for (int v = threadIdx.x; v < nvec; v += 256) {
+    const uint4 u = *(const uint4*)(xr + v * 8), wv = *(const uint4*)(w + v * 8);
+    const uint32_t e[4] = {u.x, u.y, u.z, u.w}, ww[4] = {wv.x, wv.y, wv.z, wv.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float lo = round_bf16(bf16lo(e[i]) * r), hi = round_bf16(bf16hi(e[i]) * r);
+      o[i] = pack_bf16x2(bf16lo(ww[i]) * lo, bf16hi(ww[i]) * hi);
+    }
+    *(uint4*)(yr + v * 8) = uint4{o[0], o[1], o[2], o[3]};
+  }
+}
+
+struct LmGemmArgs {
+  const uint16_t* x;  // [m, k] normalized rows
+  const uint16_t* w;  // [n, k] bf16
+  float* cand_val;    // [m, n_blocks]
+  int32_t* cand_idx;  // [m, n_blocks]
+  int m, n, k;
+  int n_blocks, m_blocks;
+};
+
+// Workgroup b: XCD b % 8 takes vocabulary blocks nb = xcd (mod 8) and runs the row blocks of each
+// such nb back to back, so repeated weight tiles come from that XCD's L2.
+__global__ __launch_bounds__(256) void lm_gemm_argmax_kernel(LmGemmArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t gsm[];
+  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+  const int nb = (slot / a.m_blocks) * 8 + xcd, mb = slot % a.m_blocks;
+  if (nb >= a.n_blocks) return;  // surplus workgroups of the rounded grid (whole workgroup)
+  uint16_t* As = gsm;                    // [2][128][kGLd]
+  uint16_t* Bs = gsm + 2 * kGBM * kGLd;  // [2][128][kGLd]
+  __shared__ float rv[2][kGBM];
+  __shared__ int32_t ri[2][kGBM];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int m0 = mb * kGBM, n0 = nb * kGBN;
+
+  // Loader role for both operands: rows tid/8 + 32i (i < 4), 8-element chunk tid%8.
+  const int lr = tid >> 3, lc = (tid & 7) * 8;
+  const uint16_t* ap[4];
+  const uint16_t* bp[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int ra = min(m0 + lr + 32 * i, a.m - 1), rb = min(n0 + lr + 32 * i, a.n - 1);  // repeats are dropped
+    ap[i] = a.x + (int64_t)ra * a.k + lc;
+    bp[i] = a.w + (int64_t)rb * a.k + lc;
+  }
+  uint4 ra0, ra1, ra2, ra3, rb0, rb1, rb2, rb3;
+#define MSA_LM_LOAD(k0)                  \
+  do {                                   \
+    ra0 = *(const uint4*)(ap[0] + (k0)); \
+    ra1 = *(const uint4*)(ap[1] + (k0)); \
+    ra2 = *(const uint4*)(ap[2] + (k0)); \
+    ra3 = *(const uint4*)(ap[3] + (k0)); \
+    rb0 = *(const uint4*)(bp[0] + (k0)); \
+    rb1 = *(const uint4*)(bp[1] + (k0)); \
+    rb2 = *(const uint4*)(bp[2] + (k0)); \
+    rb3 = *(const uint4*)(bp[3] + (k0)); \
+  } while (0)
+#define MSA_LM_STORE(buf)                                             \
+  do {                                                                \
+    uint16_t* A_ = As + (buf) * kGBM * kGLd + lr * kGLd + lc;         \
+    uint16_t* B_ = Bs + (buf) * kGBN * kGLd + lr * kGLd + lc;         \
+    *(uint4*)(A_) = ra0;                                              \
+    *(uint4*)(A_ + 32 * kGLd) = ra1;                                  \
+    *(uint4*)(A_ + 64 * kGLd) = ra2;                                  \
+    *(uint4*)(A_ + 96 * kGLd) = ra3;                                  \
+    *(uint4*)(B_) = rb0;                                              \
+    *(uint4*)(B_ + 32 * kGLd) = rb1;                                  \
+    *(uint4*)(B_ + 64 * kGLd) = rb2;                                  \
+    *(uint4*)(B_ + 96 * kGLd) = rb3;                                  \
+  } while (0)
+
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int nk = a.k / kGBK;
+  MSA_LM_LOAD(0);
+  MSA_LM_STORE(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    const bool more = kt + 1 < nk;
+    if (more) MSA_LM_LOAD((kt + 1) * kGBK);
+    const uint16_t* A = As + cur * kGBM * kGLd + (wm * 64 + j) * kGLd + g * 8;
+    const uint16_t* B = Bs + cur * kGBN * kGLd + (wn * 64 + j) * kGLd + g * 8;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      bf16x8 af[4], bfr[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        af[t] = *(const bf16x8*)(A + t * 16 * kGLd + ks * 32);
+        bfr[t] = *(const bf16x8*)(B + t * 16 * kGLd + ks * 32);
+      }
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt)
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt], bfr[nt], acc[mt][nt], 0, 0, 0);
+    }
+    if (more) MSA_LM_STORE(cur ^ 1);
+    __syncthreads();
+  }
+#undef MSA_LM_LOAD
+#undef MSA_LM_STORE
+
+  // lane (g, j) of tile (mt, nt): row wm*64 + mt*16 + 4g + i, vocabulary entry n0 + wn*64 + nt*16 + j.
+  // Per row: the lane's best over nt (increasing entries), then over the 16 lanes j, then over wn.
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float v = -INFINITY;
+      int idx = 0x7fffffff;
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        const int col = n0 + wn * 64 + nt * 16 + j;
+        const float c = col < a.n ? round_bf16(acc[mt][nt][i]) : -INFINITY;
+        if (c > v) {
+          v = c;
+          idx = col;
+        }
+      }
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) {
+        const float ov = __shfl_xor(v, off);
+        const int oi = __shfl_xor(idx, off);
+        if (ov > v || (ov == v && oi < idx)) {
+          v = ov;
+          idx = oi;
+        }
+      }
+      if (j == 0) {
+        rv[wn][wm * 64 + mt * 16 + 4 * g + i] = v;
+        ri[wn][wm * 64 + mt * 16 + 4 * g + i] = idx;
+      }
+    }
+  __syncthreads();
+  if (tid < kGBM && m0 + tid < a.m) {
+    float v = rv[0][tid];
+    int idx = ri[0][tid];
+    if (rv[1][tid] > v || (rv[1][tid] == v && ri[1][tid] < idx)) {
+      v = rv[1][tid];
+      idx = ri[1][tid];
+    }
+    a.cand_val[(int64_t)(m0 + tid) * a.n_blocks + nb] = v;
+    a.cand_idx[(int64_t)(m0 + tid) * a.n_blocks + nb] = idx;
+  }
+}
+
+int lm_gemm_vocab_blocks(int64_t vocab) { return (int)((vocab + kGBN - 1) / kGBN); }
+
+// Gather + norm into `xn` ([num_rows, k] bf16), then the GEMM writes [num_rows][n_blocks]
+// candidates. k % 64 == 0.
+int launch_lm_gemm_argmax(const uint16_t* hidden, int64_t ld_hidden, int64_t hidden_rows, const int64_t* rows,
+                          int num_rows, int k, const uint16_t* norm_w, float eps, const uint16_t* weight, int vocab,
+                          uint16_t* xn, float* cand_val, int32_t* cand_idx, hipStream_t s) {
+  hipLaunchKernelGGL(lm_rows_prologue_kernel, dim3(num_rows), dim3(256), 0, s, hidden, ld_hidden, hidden_rows, rows,
+                     norm_w, eps, k, xn);
+  int rc = check_launch("msa_lm_head_argmax (row prologue)");
+  if (rc != MSA_OK) return rc;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void*)lm_gemm_argmax_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)kGemmLds);
+    if (e != hipSuccess) return fail(MSA_ERR_LAUNCH, std::string("hipFuncSetAttribute: ") + hipGetErrorString(e));
+    attr_set = true;
+  }
+  LmGemmArgs a{};
+  a.x = xn; a.w = weight; a.cand_val = cand_val; a.cand_idx = cand_idx;
+  a.m = num_rows; a.n = vocab; a.k = k;
+  a.n_blocks = lm_gemm_vocab_blocks(vocab);
+  a.m_blocks = (num_rows + kGBM - 1) / kGBM;
+  const int blocks = ((a.n_blocks + 7) / 8) * 8 * a.m_blocks;
+  hipLaunchKernelGGL(lm_gemm_argmax_kernel, dim3(blocks), dim3(256), kGemmLds, s, a);
+  return check_launch("msa_lm_head_argmax (GEMM)");
+}
+
 }  // namespace msa
 
 using namespace msa;

@@ -120,11 +120,6 @@ __device__ __forceinline__ void block_to_tile(const RowsArgs& a, int& rb, int& m
   mc = slot % a.n_mc;
 }
 
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c, false);
-}
-
 // Stage the tile's ROWS activation rows in LDS (rows past the chunk repeat its last token), with the
 // prologue applied. NTH threads; TPT = NTH / ROWS threads per row. Two halves so the caller can
 // put other loads between them: stage_x_issue starts the first XB 16-byte vectors of each thread
@@ -817,9 +812,35 @@ extern "C" int msa_qkv_rope_cache_rows(const uint16_t* x, int64_t ldx, int64_t x
 
 constexpr int kLmBlocks = 256;  // persistent workgroups of the LM head (one per CU)
 constexpr int kLmMaxRows = 64;  // sampled rows per launch (four 16-token MFMA tiles)
+constexpr int kLmW = 8;         // wavefronts per LM-head workgroup
 
-extern "C" size_t msa_lm_head_argmax_workspace_size(int64_t num_rows, int64_t vocab) {
-  if (num_rows <= 0 || vocab <= 0) return 0;
+namespace msa {  // the GEMM route of the LM head (gemm_int8.hip)
+int lm_gemm_vocab_blocks(int64_t vocab);
+int launch_lm_gemm_argmax(const uint16_t* hidden, int64_t ld_hidden, int64_t hidden_rows, const int64_t* rows,
+                          int num_rows, int k, const uint16_t* norm_w, float eps, const uint16_t* weight, int vocab,
+                          uint16_t* xn, float* cand_val, int32_t* cand_idx, hipStream_t s);
+}  // namespace msa
+
+// 16-row activation tiles one streaming launch holds in LDS (0: not even one).
+static int64_t lm_tiles_per_launch(int64_t k) {
+  const size_t tile_bytes = (size_t)16 * (k + 8) * 2;
+  return std::min<int64_t>(kLmMaxRows / 16, (int64_t)((kMaxLds - 2 * kLmW * 64 * 4) / tile_bytes));
+}
+
+// The streaming kernel reads the whole weight once per launch of up to 64 rows; when the rows need
+// more than one launch (or one tile does not fit), the GEMM route reads it about once in all.
+static bool lm_use_gemm(int64_t num_rows, int64_t k) {
+  const int64_t tiles = lm_tiles_per_launch(k);
+  return k % 64 == 0 && (tiles < 1 || num_rows > 16 * tiles);
+}
+
+static size_t align256(size_t b) { return (b + 255) / 256 * 256; }
+
+extern "C" size_t msa_lm_head_argmax_workspace_size(int64_t num_rows, int64_t k, int64_t vocab) {
+  if (num_rows <= 0 || vocab <= 0 || k <= 0) return 0;
+  if (lm_use_gemm(num_rows, k))
+    return align256((size_t)num_rows * k * 2) +
+           (size_t)num_rows * lm_gemm_vocab_blocks(vocab) * (sizeof(float) + sizeof(int32_t));
   return (size_t)num_rows * kLmBlocks * (sizeof(float) + sizeof(int32_t));
 }
 
@@ -834,18 +855,29 @@ extern "C" int msa_lm_head_argmax(const uint16_t* hidden, int64_t ld_hidden, int
   if (k % 32 != 0) return fail(MSA_ERR_UNSUPPORTED, "msa_lm_head_argmax: hidden must be a multiple of 32");
   if (ld_hidden < k || ld_hidden % 8 != 0 || !aligned16(hidden) || !aligned16(weight) || (norm_w && !aligned16(norm_w)))
     return fail(MSA_ERR_INVALID, "msa_lm_head_argmax: hidden / weight / norm_w must be 16-byte aligned");
-  const size_t need = msa_lm_head_argmax_workspace_size(num_rows, vocab);
+  const size_t need = msa_lm_head_argmax_workspace_size(num_rows, k, vocab);
   if (!workspace || workspace_bytes < need) return fail(MSA_ERR_WORKSPACE, "msa_lm_head_argmax: workspace too small");
   if (!aligned16(workspace)) return fail(MSA_ERR_INVALID, "msa_lm_head_argmax: workspace must be 16-byte aligned");
   hipStream_t s = (hipStream_t)stream;
+  if (lm_use_gemm(num_rows, k)) {
+    uint16_t* xn = (uint16_t*)workspace;
+    const int nbk = lm_gemm_vocab_blocks(vocab);
+    float* gval = (float*)((char*)workspace + align256((size_t)num_rows * k * 2));
+    int32_t* gidx = (int32_t*)(gval + (size_t)num_rows * nbk);
+    const int rc = launch_lm_gemm_argmax(hidden, ld_hidden, hidden_rows, rows, (int)num_rows, (int)k, norm_w, eps, weight,
+                                         (int)vocab, xn, gval, gidx, s);
+    if (rc != MSA_OK) return rc;
+    hipLaunchKernelGGL(argmax_candidates_kernel, dim3((unsigned)num_rows), dim3(256), 0, s, gval, gidx, nbk, out_ids);
+    return check_launch("msa_lm_head_argmax (candidates)");
+  }
   const int64_t nch = k / 32;  // 32-wide K chunks per vocabulary row; the load ring depth divides it
   float* cand_val = (float*)workspace;
   int32_t* cand_idx = (int32_t*)((char*)workspace + (size_t)num_rows * kLmBlocks * sizeof(float));
   // Launches of up to 64 rows each (fewer when 16-row activation tiles of this width fill LDS);
   // every launch writes its rows' candidates. Each launch streams the whole weight once.
-  constexpr int W = 8;
+  constexpr int W = kLmW;
   const size_t tile_bytes = (size_t)16 * (k + 8) * 2;
-  const int64_t max_mt = std::min<int64_t>(kLmMaxRows / 16, (int64_t)((kMaxLds - 2 * W * 64 * 4) / tile_bytes));
+  const int64_t max_mt = lm_tiles_per_launch(k);
   if (max_mt < 1) return fail(MSA_ERR_UNSUPPORTED, "msa_lm_head_argmax: hidden too large for the LDS activation tile");
   for (int64_t r0 = 0; r0 < num_rows; r0 += 16 * max_mt) {
     const int nr = (int)std::min<int64_t>(16 * max_mt, num_rows - r0);

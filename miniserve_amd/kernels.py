@@ -465,7 +465,7 @@ def lm_head_argmax(
     r = rows.numel()
     vocab, k = weight.shape
     out = torch.empty(r, dtype=torch.int64, device=hidden.device)
-    ws_bytes = _native.query("msa_lm_head_argmax_workspace_size", r, vocab) if r else 0
+    ws_bytes = _native.query("msa_lm_head_argmax_workspace_size", r, k, vocab) if r else 0
     ws = workspaces.get("lm_head", hidden.device, ws_bytes)
     _native.call(
         "msa_lm_head_argmax", _ptr(hidden), hidden.stride(0), hidden.shape[0], _ptr(rows), r, k,

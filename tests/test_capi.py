@@ -80,6 +80,12 @@ def test_workspace_sizes():
     assert _native.query("msa_int8_linear_workspace_size", 64, 1024, 2048) == 0  # token-split kernel
     assert _native.query("msa_int8_linear_workspace_size", 256, 1024, 2048) == 0  # LDS-tiled GEMM
     assert _native.query("msa_int8_linear_workspace_size", 64, 1024, 2000) > 0  # K % 64 != 0: split-K
+    # LM head: up to 64 rows stream the weight (candidates of 256 workgroups); more rows take the
+    # GEMM route (normalized rows + candidates of 128-entry vocabulary blocks)
+    assert _native.query("msa_lm_head_argmax_workspace_size", 64, 1024, 151936) == 64 * 256 * 8
+    assert _native.query("msa_lm_head_argmax_workspace_size", 65, 1024, 151936) == 65 * 1024 * 2 + 65 * 1187 * 8
+    assert _native.query("msa_lm_head_argmax_workspace_size", 17, 4096, 151936) == 17 * 4096 * 2 + 17 * 1187 * 8
+    assert _native.query("msa_lm_head_argmax_workspace_size", 16, 4096, 151936) == 16 * 256 * 8
     assert _native.query("msa_paged_attention_decode_workspace_size", 64, 16, 128, 1) == 0
     ws = _native.query("msa_paged_attention_decode_workspace_size", 64, 16, 128, 8)
     assert ws >= 64 * 16 * 8 * (128 + 2) * 4

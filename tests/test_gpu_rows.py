@@ -194,7 +194,11 @@ def _check_greedy(got, logits_bf16):
     return int((got == ref).sum())
 
 
-@pytest.mark.parametrize("rows,vocab,k", [(64, 151936, 1024), (1, 32771, 1024), (17, 5000, 256), (40, 9000, 4096)])
+# (64, 151936, 1024): the decode step; up to 64 rows (16 at k = 4096) stream the weight with the rows
+# in LDS. More rows take the GEMM route: 65 rows (a chunked-prefill step's samples), 130 rows, and
+# 200 rows at an 8B-sized hidden width.
+@pytest.mark.parametrize("rows,vocab,k", [(64, 151936, 1024), (1, 32771, 1024), (17, 5000, 256), (40, 9000, 4096),
+                                          (65, 151936, 1024), (130, 9000, 1024), (200, 12000, 4096)])
 def test_lm_head_argmax(rows, vocab, k):
     hidden, w, nw, sel = _lm_case(rows, vocab, k, seed=rows + vocab % 97)
     got = kernels.lm_head_argmax(hidden.to(DEV), sel.to(DEV), nw.to(DEV), 1e-6, w.to(DEV)).cpu()
@@ -208,8 +212,9 @@ def test_lm_head_argmax(rows, vocab, k):
     assert torch.equal(got, got2)
 
 
-def test_lm_head_argmax_first_index_wins_ties():
-    rows, vocab, k = 8, 20000, 1024
+@pytest.mark.parametrize("rows", [8, 100])  # the streaming route and the GEMM route
+def test_lm_head_argmax_first_index_wins_ties(rows):
+    vocab, k = 20000, 1024
     hidden, w, nw, sel = _lm_case(rows, vocab, k, seed=5)
     h = ol.rms_norm(hidden[sel], nw, 1e-6)
     # plant the same winning row at three vocabulary positions, spread over row blocks and tiles
