@@ -34,7 +34,12 @@ struct GemmArgs {
   int64_t ldr;
   int m, n, k;
   int n_blocks;  // weight-row blocks (of 128 rows, or 64 gate + 64 up for SILU_MUL)
+  int m_blocks;  // token blocks of 128
+  int k_per;     // K per split (a multiple of 64; == k without split-K)
+  float* part;   // split-K: float32 partials [splits][m][n]
 };
+
+constexpr int kEpiPartial = 3;  // split-K: store the float32 accumulators, no rounding
 
 __device__ __forceinline__ bf16x8 gemm_dequant8(uint32_t lo, uint32_t hi, float s) {
   bf16x8 r;
@@ -69,8 +74,10 @@ __global__ __launch_bounds__(256) void int8_gemm_kernel(GemmArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int j = lane & 15, g = lane >> 4;
   const int wm = wave >> 1, wn = wave & 1;
-  const int nb = blockIdx.x % a.n_blocks, mb = blockIdx.x / a.n_blocks;
+  const int nb = blockIdx.x % a.n_blocks, rest = blockIdx.x / a.n_blocks;
+  const int mb = rest % a.m_blocks, ks = rest / a.m_blocks;  // ks: the split of K (0 without split-K)
   const int m0 = mb * kGBM;
+  const int64_t kbase = (int64_t)ks * a.k_per;
 
   // Loader roles. A: rows tid/8 + 32i (i < 4), 8-element chunk tid%8. B: rows tid/4 + 64i (i < 2),
   // 16-element chunk tid%4.
@@ -80,7 +87,7 @@ __global__ __launch_bounds__(256) void int8_gemm_kernel(GemmArgs a) {
   for (int i = 0; i < 4; ++i) {
     int row = m0 + ar + 32 * i;
     row = row < a.m ? row : a.m - 1;  // rows past m repeat row m-1; their outputs are dropped
-    ap[i] = a.x + (int64_t)row * a.ldx + ac;
+    ap[i] = a.x + (int64_t)row * a.ldx + kbase + ac;
   }
   const int br = tid >> 2, bc = (tid & 3) * 16;
   const int8_t* bp[2];
@@ -89,7 +96,7 @@ __global__ __launch_bounds__(256) void int8_gemm_kernel(GemmArgs a) {
   for (int i = 0; i < 2; ++i) {
     int row = gemm_wrow<EPI>(a, nb, br + 64 * i);
     row = row < a.n ? row : a.n - 1;
-    bp[i] = a.w + (int64_t)row * a.k + bc;
+    bp[i] = a.w + (int64_t)row * a.k + kbase + bc;
     bs[i] = bf16_to_f32(a.scale[row]);
   }
   uint4 ra0, ra1, ra2, ra3, rb0, rb1;  // the next K step's tiles, in flight during the MFMAs
@@ -122,7 +129,7 @@ __global__ __launch_bounds__(256) void int8_gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int nk = a.k / kGBK;
+  const int nk = a.k_per / kGBK;
   MSA_GEMM_LOAD(0);
   MSA_GEMM_STORE(0);
   __syncthreads();
@@ -159,7 +166,14 @@ __global__ __launch_bounds__(256) void int8_gemm_kernel(GemmArgs a) {
     for (int i = 0; i < 4; ++i) {
       const int tok = m0 + wm * 64 + mt * 16 + 4 * g + i;
       if (tok >= a.m) continue;
-      if constexpr (EPI == MSA_EPI_SILU_MUL) {
+      if constexpr (EPI == kEpiPartial) {
+        float* prow = a.part + ((int64_t)ks * a.m + tok) * a.n;
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) {
+          const int col = nb * kGBN + wn * 64 + nt * 16 + j;
+          if (col < a.n) prow[col] = acc[mt][nt][i];
+        }
+      } else if constexpr (EPI == MSA_EPI_SILU_MUL) {
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
           const int col = nb * 64 + wn * 32 + nt * 16 + j;
@@ -191,6 +205,79 @@ static int launch_gemm(const GemmArgs& a, int blocks, hipStream_t s) {
   }
   hipLaunchKernelGGL(int8_gemm_kernel<EPI>, dim3(blocks), dim3(256), kGemmLds, s, a);
   return MSA_OK;
+}
+
+// Split-K merge: y = bf16(sum of the splits' partials in split order), then the residual add
+// bf16(residual + y) when given (in place allowed: each thread reads its residual before writing).
+__global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __restrict__ part, int splits, int m,
+                                                                 int n, uint16_t* y, int64_t ldy, const uint16_t* resid,
+                                                                 int64_t ldr) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)m * n) return;
+  const int tok = (int)(idx / n), col = (int)(idx % n);
+  float v = 0.f;
+  for (int s = 0; s < splits; ++s) v += part[((int64_t)s * m + tok) * n + col];
+  v = round_bf16(v);
+  if (resid) v += bf16_to_f32(resid[(int64_t)tok * ldr + col]);
+  y[(int64_t)tok * ldy + col] = f32_to_bf16(v);
+}
+
+// K splits of the GEMM: 1 when the output tiles fill the GPU (or for silu * up), else the fewest
+// splits (of whole 64-wide steps, at least 512 of K each, at most 8) that give 256+ workgroups,
+// or the most such splits when none does.
+int gemm_splits(int64_t m, int64_t n, int64_t k, int epilogue) {
+  if (epilogue == MSA_EPI_SILU_MUL || k % kGBK != 0) return 1;
+  const int64_t tiles = ((n + kGBN - 1) / kGBN) * ((m + kGBM - 1) / kGBM);
+  if (tiles >= 192) return 1;
+  const int64_t steps = k / kGBK;
+  int best = 1;
+  for (int s = 2; s <= 8; ++s) {
+    if (steps % s != 0 || k / s < 512) continue;
+    best = s;
+    if (tiles * s >= 256) break;
+  }
+  return best;
+}
+
+size_t gemm_workspace_size(int64_t m, int64_t n, int64_t k, int epilogue) {
+  const int s = gemm_splits(m, n, k, epilogue);
+  return s > 1 ? (size_t)s * m * n * sizeof(float) : 0;
+}
+
+// The GEMM with arguments checked by the caller; split-K when planned and the workspace holds it.
+int gemm_run(const uint16_t* x, int64_t m, int64_t k, int64_t ldx, const int8_t* qweight, const uint16_t* scale,
+             int64_t n, uint16_t* y, int64_t ldy, int epilogue, const uint16_t* residual, int64_t ldr, void* workspace,
+             size_t workspace_bytes, hipStream_t s) {
+  GemmArgs a{};
+  a.x = x; a.ldx = ldx; a.w = qweight; a.scale = scale; a.y = y; a.ldy = ldy; a.resid = residual; a.ldr = ldr;
+  a.m = (int)m; a.n = (int)n; a.k = (int)k;
+  a.n_blocks = (int)(epilogue == MSA_EPI_SILU_MUL ? (n / 2 + 63) / 64 : (n + kGBN - 1) / kGBN);
+  a.m_blocks = (int)((m + kGBM - 1) / kGBM);
+  int splits = gemm_splits(m, n, k, epilogue);
+  if (splits > 1 && (!workspace || workspace_bytes < gemm_workspace_size(m, n, k, epilogue) || !aligned16(workspace)))
+    splits = 1;
+  a.k_per = (int)(k / splits);
+  a.part = (float*)workspace;
+  const int64_t blocks = (int64_t)a.n_blocks * a.m_blocks * splits;
+  if (blocks > 0x7fffffff) return fail(MSA_ERR_INVALID, "msa_int8_gemm: too many tiles");
+  int rc;
+  if (splits > 1) {
+    rc = launch_gemm<kEpiPartial>(a, (int)blocks, s);
+    if (rc != MSA_OK) return rc;
+    rc = check_launch("msa_int8_gemm (split-K)");
+    if (rc != MSA_OK) return rc;
+    const int64_t elems = m * n;
+    hipLaunchKernelGGL(gemm_splitk_reduce_kernel, dim3((unsigned)((elems + 255) / 256)), dim3(256), 0, s, a.part,
+                       splits, a.m, a.n, y, ldy, epilogue == MSA_EPI_RESIDUAL ? residual : nullptr, ldr);
+    return check_launch("msa_int8_gemm (split-K merge)");
+  }
+  switch (epilogue) {
+    case MSA_EPI_NONE: rc = launch_gemm<MSA_EPI_NONE>(a, (int)blocks, s); break;
+    case MSA_EPI_SILU_MUL: rc = launch_gemm<MSA_EPI_SILU_MUL>(a, (int)blocks, s); break;
+    default: rc = launch_gemm<MSA_EPI_RESIDUAL>(a, (int)blocks, s); break;
+  }
+  if (rc != MSA_OK) return rc;
+  return check_launch("msa_int8_gemm");
 }
 
 // ---- LM head for many rows: gather + RMSNorm once, then a bf16 GEMM with an argmax epilogue ----
@@ -433,19 +520,5 @@ extern "C" int msa_int8_gemm(const uint16_t* x, int64_t m, int64_t k, int64_t ld
   if (ldy < out_cols) return fail(MSA_ERR_INVALID, "msa_int8_gemm: ldy too small");
   if (epilogue == MSA_EPI_RESIDUAL && (!residual || ldr < n))
     return fail(MSA_ERR_INVALID, "msa_int8_gemm: the residual epilogue needs residual with ldr >= n");
-  GemmArgs a{};
-  a.x = x; a.ldx = ldx; a.w = qweight; a.scale = scale; a.y = y; a.ldy = ldy; a.resid = residual; a.ldr = ldr;
-  a.m = (int)m; a.n = (int)n; a.k = (int)k;
-  a.n_blocks = (int)(epilogue == MSA_EPI_SILU_MUL ? (n / 2 + 63) / 64 : (n + kGBN - 1) / kGBN);
-  const int64_t blocks = (int64_t)a.n_blocks * ((m + kGBM - 1) / kGBM);
-  if (blocks > 0x7fffffff) return fail(MSA_ERR_INVALID, "msa_int8_gemm: too many tiles");
-  hipStream_t s = (hipStream_t)stream;
-  int rc;
-  switch (epilogue) {
-    case MSA_EPI_NONE: rc = launch_gemm<MSA_EPI_NONE>(a, (int)blocks, s); break;
-    case MSA_EPI_SILU_MUL: rc = launch_gemm<MSA_EPI_SILU_MUL>(a, (int)blocks, s); break;
-    default: rc = launch_gemm<MSA_EPI_RESIDUAL>(a, (int)blocks, s); break;
-  }
-  if (rc != MSA_OK) return rc;
-  return check_launch("msa_int8_gemm");
+  return gemm_run(x, m, k, ldx, qweight, scale, n, y, ldy, epilogue, residual, ldr, nullptr, 0, (hipStream_t)stream);
 }

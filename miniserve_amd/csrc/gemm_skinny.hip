@@ -276,9 +276,16 @@ extern "C" int msa_int8_linear_rows(const uint16_t* x, int64_t ldx, int64_t m, i
 // Smaller batches whose activation tile fits in LDS go to the token-split kernels (gemv_rows.hip).
 static bool rows_fits(int64_t k) { return k % 64 == 0 && 16 * (k + 8) * 2 + 16 * 1024 <= 160 * 1024; }
 
+namespace msa {  // the LDS-tiled GEMM route (gemm_int8.hip)
+int gemm_run(const uint16_t* x, int64_t m, int64_t k, int64_t ldx, const int8_t* qweight, const uint16_t* scale,
+             int64_t n, uint16_t* y, int64_t ldy, int epilogue, const uint16_t* residual, int64_t ldr, void* workspace,
+             size_t workspace_bytes, hipStream_t s);
+size_t gemm_workspace_size(int64_t m, int64_t n, int64_t k, int epilogue);
+}  // namespace msa
+
 extern "C" size_t msa_int8_linear_workspace_size(int64_t m, int64_t n, int64_t k) {
   if (m <= 0 || n <= 0 || k <= 0) return 0;
-  if (m >= kGemmMinRows && k % 64 == 0) return 0;
+  if (m >= kGemmMinRows && k % 64 == 0) return msa::gemm_workspace_size(m, n, k, MSA_EPI_NONE);  // split-K partials
   if (rows_fits(k)) return 0;
   size_t best = 0;
   for (int epi = 0; epi < 3; ++epi) {
@@ -305,7 +312,8 @@ extern "C" int msa_int8_linear(const uint16_t* x, int64_t m, int64_t k, int64_t 
   if (epilogue == MSA_EPI_RESIDUAL && (!residual || ldr < n))
     return fail(MSA_ERR_INVALID, "msa_int8_linear: residual epilogue needs residual with ldr >= n");
   if (m >= kGemmMinRows && k % 64 == 0)
-    return msa_int8_gemm(x, m, k, ldx, qweight, scale, n, y, ldy, epilogue, residual, ldr, stream);
+    return gemm_run(x, m, k, ldx, qweight, scale, n, y, ldy, epilogue, residual, ldr, workspace, workspace_bytes,
+                    (hipStream_t)stream);
   if (rows_fits(k))
     return msa_int8_linear_rows(x, ldx, m, k, nullptr, 0.f, qweight, scale, n, epilogue, y, ldy, residual, ldr, stream);
 
