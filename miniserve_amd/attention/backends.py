@@ -86,7 +86,11 @@ def build_attention_metadata(chunks: list[SeqChunk], slot_mapping: Tensor, block
     if block_size != 16:
         raise RuntimeError("the HIP attention kernels use 16-token blocks")
     device = slot_mapping.device
-    dec = [c for c in chunks if c.num_new == 1]
+    # Longest work first: workgroups are dispatched in grid order, so a long sequence (or a late
+    # causal tile with many keys) queued last would run alone at the end. Each decode sequence
+    # carries its own output row and each prefill work item its own sequence and tile, so the
+    # order changes no result.
+    dec = sorted((c for c in chunks if c.num_new == 1), key=lambda c: -c.context_len)
     pre = [c for c in chunks if c.num_new > 1]
     parts: list[np.ndarray] = []
     layout: list[tuple[str, tuple[int, ...]]] = []
@@ -118,7 +122,8 @@ def build_attention_metadata(chunks: list[SeqChunk], slot_mapping: Tensor, block
         add("p_info", np.array([[c.flat_start, c.num_new, c.num_cached] for c in pre], dtype=np.int32))
         add("p_tables", tables)
         for tile in PREFILL_TILES:
-            work = [(i, t0) for i, c in enumerate(pre) for t0 in range(0, c.num_new, tile)]
+            work = sorted(((i, t0) for i, c in enumerate(pre) for t0 in range(0, c.num_new, tile)),
+                          key=lambda w: -(pre[w[0]].num_cached + min(w[1] + tile, pre[w[0]].num_new)))
             add(f"p_work{tile}", np.array(work, dtype=np.int32).reshape(-1, 2))
 
     views: dict[str, Tensor] = {}

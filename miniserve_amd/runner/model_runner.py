@@ -85,15 +85,22 @@ class CapturedDecode:
 
     def run(self, scheduled: list[ScheduledChunk], block_size: int) -> list[int]:
         b = self.batch
+        # Attention plan rows longest context first (each keeps its own q row), as
+        # build_attention_metadata orders them.
+        order = sorted(range(b), key=lambda i: -scheduled[i].num_computed)
         for i, s in enumerate(scheduled):
             p = s.num_computed
             table = s.block_table
             self.host_i64[i] = s.token_ids[p]
             self.host_i64[b + i] = p
             self.host_i64[2 * b + i] = table[p // block_size] * block_size + p % block_size
-            self.host_meta[b + i] = p + 1
+        for r, i in enumerate(order):
+            s = scheduled[i]
+            p = s.num_computed
+            self.host_meta[r] = i
+            self.host_meta[b + r] = p + 1
             need = -(-(p + 1) // block_size)
-            self.host_meta[2 * b + i * self.max_blocks : 2 * b + i * self.max_blocks + need] = table[:need]
+            self.host_meta[2 * b + r * self.max_blocks : 2 * b + r * self.max_blocks + need] = s.block_table[:need]
         self.dev.copy_(self.host, non_blocking=True)
         self.graph.replay()
         return self.out_ids.tolist()  # the one device -> host sync
