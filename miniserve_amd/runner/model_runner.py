@@ -67,6 +67,7 @@ class CapturedDecode:
         self.host_meta = self.host[3 * b :].view(torch.int32).numpy()
         self.host_i64 = self.host[: 3 * b].numpy()
         self.host_meta[:b] = np.arange(b, dtype=np.int32)
+        self.tables_written: list[list[int] | None] = [None] * b  # table prefix held by each plan row
         self.host_meta[b : 2 * b] = 1
         self.host_i64[2 * b : 3 * b] = -1  # warm-up rows write no KV slot (kernels skip slot < 0)
         self.dev.copy_(self.host)
@@ -84,23 +85,28 @@ class CapturedDecode:
             self.out_ids = model.greedy(self.ids, self.pos, runner.kv_caches, self.meta, self.rows)
 
     def run(self, scheduled: list[ScheduledChunk], block_size: int) -> list[int]:
-        b = self.batch
+        b, bs, mb = self.batch, block_size, self.max_blocks
+        hi, hm = self.host_i64, self.host_meta
+        pos = [s.num_computed for s in scheduled]
+        hi[:b] = [s.token_ids[p] for s, p in zip(scheduled, pos, strict=True)]
+        hi[b : 2 * b] = pos
+        hi[2 * b : 3 * b] = [s.block_table[p // bs] * bs + p % bs for s, p in zip(scheduled, pos, strict=True)]
         # Attention plan rows longest context first (each keeps its own q row), as
         # build_attention_metadata orders them.
-        order = sorted(range(b), key=lambda i: -scheduled[i].num_computed)
-        for i, s in enumerate(scheduled):
-            p = s.num_computed
-            table = s.block_table
-            self.host_i64[i] = s.token_ids[p]
-            self.host_i64[b + i] = p
-            self.host_i64[2 * b + i] = table[p // block_size] * block_size + p % block_size
+        order = sorted(range(b), key=pos.__getitem__, reverse=True)
+        hm[:b] = order
+        hm[b : 2 * b] = [pos[i] + 1 for i in order]
+        # A table row is rewritten only when its contents changed since the last step: comparing
+        # two short lists costs far less than converting one into the buffer.
+        written = self.tables_written
         for r, i in enumerate(order):
-            s = scheduled[i]
-            p = s.num_computed
-            self.host_meta[r] = i
-            self.host_meta[b + r] = p + 1
-            need = -(-(p + 1) // block_size)
-            self.host_meta[2 * b + r * self.max_blocks : 2 * b + r * self.max_blocks + need] = s.block_table[:need]
+            need = (pos[i] + bs) // bs
+            row = scheduled[i].block_table[:need]
+            if len(row) != need:
+                raise RuntimeError(f"block table of {len(row)} blocks is shorter than context {pos[i] + 1}")
+            if written[r] != row:
+                hm[2 * b + r * mb : 2 * b + r * mb + len(row)] = row
+                written[r] = row
         self.dev.copy_(self.host, non_blocking=True)
         self.graph.replay()
         return self.out_ids.tolist()  # the one device -> host sync
