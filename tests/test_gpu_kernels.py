@@ -266,6 +266,22 @@ def test_prefill_attention(heads, kv_heads):
     assert rel_l2(out, dense) < 1e-2
 
 
+@pytest.mark.parametrize("heads,kv_heads", [(16, 8), (32, 8)])
+def test_speculative_verify_batch(heads, kv_heads):
+    """Every sequence verifies 1-7 drafts (2-8 new tokens after 200-900 cached keys, the
+    reference's grouped short-query rows, backends.py:101-132), mixed with plain decodes."""
+    rng = random.Random(heads + 7)
+    specs = [(rng.randint(200, 900), rng.randint(2, 8)) for _ in range(40)] + [(rng.randint(1, 500), 1) for _ in range(8)]
+    out, ref, dense = _run_both(specs, heads, kv_heads, seed=heads + 7)
+    assert rel_l2(out, ref) < 1e-2
+    assert rel_l2(out, dense) < 1e-2
+    row = 0
+    for cached, new in specs:  # every sequence on its own, first and last verified token
+        for r in (row, row + new - 1):
+            assert rel_l2(out[r], ref[r]) < 1e-2, (cached, new)
+        row += new
+
+
 def test_mixed_decode_and_prefill_batch():
     """Decodes first, then one long fresh chunk -- the chunked-prefill step's flat order."""
     rng = random.Random(4)
