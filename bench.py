@@ -16,6 +16,7 @@ Other workloads (each prints its own JSON line):
   prefill    chunked-prefill step: one 1984-token prompt chunk + 64 decodes (contexts U[64, 1024])
              on the same 0.6B model -> tok/s
   decode8b   Qwen3-8B-shaped int8 decode, 256 tokens, contexts U[512, 4096] -> tok/s
+  sample     temperature / top-k / top-p sampling of 64 rows of 151936 logits -> rows/s
 
 Every line carries ``roofline`` for the workload's dominant kernel (algorithmic bytes or flops per
 launch / its average duration, HIP events on the launch stream, inputs rotated past the 256 MB
@@ -567,8 +568,49 @@ def kernel_only(mode: str, seed: int) -> int:
     return 0
 
 
+def bench_sample(args) -> dict:
+    """Sampling of a decode batch: 64 rows of Qwen3 vocabulary logits, temperature 0.8, top-k 50
+    and top-p 0.9 on every row, the exponential race on Exp(1) noise -> ids."""
+    import torch
+
+    from miniserve_amd import kernels
+
+    dev = torch.device("cuda:0")
+    rows, vocab = BATCH, 151936
+    copies = 8  # 8 x 78 MB of logits + noise: repeats cannot come from the Infinity Cache
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    logits = [torch.randn(rows, vocab, generator=g, device=dev) * 3 for _ in range(copies)]
+    noise = [torch.empty(rows, vocab, device=dev).exponential_(generator=g) for _ in range(copies)]
+    temps = torch.full((rows,), 0.8, device=dev)
+    top_k = torch.full((rows,), 50, dtype=torch.int32, device=dev)
+    top_p = torch.full((rows,), 0.9, device=dev)
+    greedy = torch.zeros(rows, dtype=torch.uint8, device=dev)
+
+    def launch(i):
+        kernels.sample_ids(logits[i], temps, top_k, top_p, greedy, noise[i])
+
+    secs = hip_time(launch, copies)
+    nbytes = 2 * rows * vocab * 4  # logits and noise, read once each
+    gbs = nbytes / secs / 1e9
+    log(f"sampling {rows} x {vocab}: {secs * 1e6:.1f} us/launch")
+    out = line("sampling tok/s (64 rows x 151936 vocab, temperature + top-k 50 + top-p 0.9)", rows / secs, "tok/s", args,
+               secs * 1e3, {"workload": "runner/sampler.py sample() on float32 logits with caller noise",
+                            "rows": rows, "vocab": vocab, "temperature": 0.8, "top_k": 50, "top_p": 0.9})
+    out["roofline"] = roofline("sample_rows_kernel", "hbm", gbs, nbytes, secs)
+    if not args.no_cpu_baseline:
+        from oracle import sampler as osm
+
+        torch.set_num_threads(cpu_threads())
+        lc, nc = logits[0].cpu(), noise[0].cpu()
+        tc, kc, pc, gc = temps.cpu(), top_k.cpu().long(), top_p.cpu(), greedy.cpu().bool()
+        med, reps = cpu_time(lambda: osm.sample(lc, tc, kc, pc, gc, nc), budget_s=15.0, max_reps=20)
+        out["cpu_baseline"] = cpu_fields(rows / med, "tok/s", f"the same 64 rows on the CPU oracle (the reference's "
+                                         f"sort-based top-k / top-p), median of {reps}")
+    return out
+
+
 WORKLOADS = {"decode": bench_decode, "linear": bench_linear, "attention": bench_attention, "prefill": bench_prefill,
-             "decode8b": bench_decode8b}
+             "decode8b": bench_decode8b, "sample": bench_sample}
 
 
 def main() -> int:

@@ -210,6 +210,31 @@ int msa_paged_attention_prefill(const uint16_t* q, int64_t ldq, const uint16_t* 
                                 const int32_t* seq_info, const int32_t* work, int num_work, float scale,
                                 uint16_t* out, int64_t ldo, msa_stream_t stream);
 
+/* ---- sampling (runner/sampler.py) ------------------------------------------------------------ */
+
+/* apply_top_k_top_p (runner/sampler.py:12-27) without a sort: out[r] = logits[r] where the entry
+ * is among the row's top_k[r] largest (ties with the k-th kept) and inside its top_p[r] nucleus
+ * (the smallest-value entries are dropped while their cumulative softmax probability stays
+ * <= 1 - p; the largest entry is always kept), -inf elsewhere. top_k[r] outside (0, vocab) or a
+ * NULL top_k: no top-k; top_p[r] >= 1 or a NULL top_p: no top-p. logits / out float32, row
+ * strides ld / ldo. */
+int msa_top_k_top_p_mask(const float* logits, int64_t ld, int64_t rows, int64_t vocab, const int32_t* top_k,
+                         const float* top_p, float* out, int64_t ldo, msa_stream_t stream);
+
+/* compute_probs (runner/sampler.py:30-40): probs[r] = softmax over the kept entries of
+ * logits[r] / temperature[r] (temperature already clamped to >= 1e-5 by the caller; NULL: 1),
+ * with top-k / top-p applied to the scaled logits as in msa_top_k_top_p_mask; 0 elsewhere. */
+int msa_sampling_probs(const float* logits, int64_t ld, int64_t rows, int64_t vocab, const float* temperature,
+                       const int32_t* top_k, const float* top_p, float* probs, int64_t ldp, msa_stream_t stream);
+
+/* sample (runner/sampler.py:55-69): out_ids[r] = argmax(logits[r]) (first index) where
+ * greedy[r] != 0, else the exponential race argmax_i probs[r][i] / max(noise[r][i], FLT_MIN) with
+ * probs as msa_sampling_probs and noise ~ Exp(1) [rows, ldn] drawn by the caller (the reference
+ * draws it with torch's exponential_, per-row generators for seeded requests). */
+int msa_sample(const float* logits, int64_t ld, int64_t rows, int64_t vocab, const float* temperature,
+               const int32_t* top_k, const float* top_p, const uint8_t* greedy, const float* noise, int64_t ldn,
+               int64_t* out_ids, msa_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

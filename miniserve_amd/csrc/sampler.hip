@@ -1,0 +1,312 @@
+// Temperature / top-k / top-p sampling without a vocabulary sort (runner/sampler.py of the
+// reference: apply_top_k_top_p, compute_probs, sample).
+//
+// One workgroup of 1024 threads per row; the row's logits stay in global memory (L2 / Infinity
+// Cache) and are re-read by each pass:
+//  1. z = logits / temperature (IEEE division, as `logits / temps`), the row maximum m, and for a
+//     greedy row the first index of the largest raw logit (`logits.argmax`).
+//  2. top-k (0 < k < vocab): the k-th largest z by radix select over order-preserving 32-bit keys,
+//     four 8-bit digits, integer counts in LDS. Every z >= that value is kept (the reference masks
+//     `sorted < kth`).
+//  3. top-p (p < 1): the reference sorts the kept logits ascending, takes the cumulative softmax
+//     and drops every token whose cumulative probability is <= 1 - p (never the largest). The same
+//     cut is found by a radix select on probability mass: the smallest key whose mass at or below
+//     it exceeds (1 - p), with each token's mass exp(z - m) / Z in 2^-44 fixed point and 64-bit
+//     integer sums (exact, order-free). Tokens of equal value are kept or dropped together.
+//  4. One output pass over the kept set K, with Z_K = sum over K of exp(z - m):
+//     MASK   out = z on K, -inf elsewhere            (apply_top_k_top_p; temperature 1)
+//     PROBS  out = exp(z - m) / Z_K on K, 0 elsewhere  (compute_probs)
+//     SAMPLE id  = first argmax over K of (exp(z - m) / Z_K) / noise  (the exponential race of
+//            `sample`, noise ~ Exp(1) supplied by the caller), or the greedy id.
+// Float sums (Z) are per-thread in a fixed order, then a fixed tree: deterministic.
+#include <hip/hip_runtime.h>
+
+#include "common.h"
+
+namespace msa {
+
+constexpr int kSampThreads = 1024;
+constexpr int kSampWaves = kSampThreads / 64;
+constexpr double kMassScale = 17592186044416.0;  // 2^44: mass fixed point (sum of <= 2^31 values < 2^64)
+
+enum SampMode { SAMP_MASK = 0, SAMP_PROBS = 1, SAMP_SAMPLE = 2 };
+
+struct SampArgs {
+  const float* logits;
+  int64_t ld;
+  int64_t vocab;
+  const float* temperature;  // null: 1
+  const int32_t* top_k;      // null or k outside (0, vocab): no top-k
+  const float* top_p;        // null or p >= 1: no top-p
+  const uint8_t* greedy;     // SAMPLE: nonzero rows take the greedy id
+  const float* noise;        // SAMPLE: [rows][ldn]
+  int64_t ldn;
+  float* out;  // MASK / PROBS: [rows][ldo]
+  int64_t ldo;
+  int64_t* ids;  // SAMPLE: [rows]
+  int mode;
+};
+
+// Order-preserving key: unsigned comparison of keys = float comparison (finite values, +-inf).
+__device__ __forceinline__ uint32_t ord_key(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+struct SampShared {
+  union {
+    uint32_t cnt[256];
+    unsigned long long mass[256];
+  } hist;
+  float fred[kSampWaves];
+  int ired[kSampWaves];
+  uint32_t bcast_u[2];
+  unsigned long long bcast_ull;
+};
+
+__device__ __forceinline__ float block_max(float v, SampShared& sh) {
+  v = fmaxf(v, __shfl_xor(v, 1));
+  v = fmaxf(v, __shfl_xor(v, 2));
+  v = fmaxf(v, __shfl_xor(v, 4));
+  v = fmaxf(v, __shfl_xor(v, 8));
+  v = fmaxf(v, __shfl_xor(v, 16));
+  v = fmaxf(v, __shfl_xor(v, 32));
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) sh.fred[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float r = sh.fred[0];
+  for (int w = 1; w < kSampWaves; ++w) r = fmaxf(r, sh.fred[w]);
+  return r;
+}
+
+__device__ __forceinline__ float block_sum(float v, SampShared& sh) {
+  for (int off = 1; off < 64; off <<= 1) v += __shfl_xor(v, off);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) sh.fred[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float r = 0.f;
+  for (int w = 0; w < kSampWaves; ++w) r += sh.fred[w];  // fixed order
+  return r;
+}
+
+// First index of the largest value: (v, i) pairs, larger v wins, equal v -> smaller i.
+__device__ __forceinline__ int block_argmax(float v, int i, SampShared& sh) {
+  for (int off = 1; off < 64; off <<= 1) {
+    const float ov = __shfl_xor(v, off);
+    const int oi = __shfl_xor(i, off);
+    if (ov > v || (ov == v && oi < i)) {
+      v = ov;
+      i = oi;
+    }
+  }
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) {
+    sh.fred[threadIdx.x >> 6] = v;
+    sh.ired[threadIdx.x >> 6] = i;
+  }
+  __syncthreads();
+  float bv = sh.fred[0];
+  int bi = sh.ired[0];
+  for (int w = 1; w < kSampWaves; ++w)
+    if (sh.fred[w] > bv || (sh.fred[w] == bv && sh.ired[w] < bi)) {
+      bv = sh.fred[w];
+      bi = sh.ired[w];
+    }
+  return bi;
+}
+
+__global__ __launch_bounds__(kSampThreads) void sample_rows_kernel(SampArgs a) {
+  __shared__ SampShared sh;
+  const int64_t row = blockIdx.x;
+  const float* lg = a.logits + row * a.ld;
+  const int64_t V = a.vocab;
+  const int tid = threadIdx.x;
+
+  if (a.mode == SAMP_SAMPLE && a.greedy && a.greedy[row]) {
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int64_t i = tid; i < V; i += kSampThreads) {
+      const float v = lg[i];
+      if (v > bv) {  // ascending i: the first of equal maxima stays
+        bv = v;
+        bi = (int)i;
+      }
+    }
+    const int id = block_argmax(bv, bi, sh);
+    if (tid == 0) a.ids[row] = id == 0x7fffffff ? 0 : id;  // a row of -inf: index 0, as argmax
+    return;
+  }
+
+  const float t = a.temperature ? a.temperature[row] : 1.0f;
+  float mloc = -INFINITY;
+  for (int64_t i = tid; i < V; i += kSampThreads) mloc = fmaxf(mloc, lg[i] / t);
+  const float m = block_max(mloc, sh);
+
+  // ---- top-k: key of the k-th largest z -----------------------------------------------------
+  uint32_t kmin = 0;  // keep z with ord_key(z) >= kmin
+  const int64_t k = a.top_k ? a.top_k[row] : 0;
+  if (k > 0 && k < V) {
+    uint32_t prefix = 0, pmask = 0;
+    int64_t remaining = k;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+      for (int b = tid; b < 256; b += kSampThreads) sh.hist.cnt[b] = 0;
+      __syncthreads();
+      for (int64_t i = tid; i < V; i += kSampThreads) {
+        const uint32_t key = ord_key(lg[i] / t);
+        if ((key & pmask) == prefix) atomicAdd(&sh.hist.cnt[(key >> shift) & 255], 1u);
+      }
+      __syncthreads();
+      if (tid == 0) {
+        int64_t above = 0;
+        int d = 255;
+        for (; d > 0; --d) {
+          if (above + (int64_t)sh.hist.cnt[d] >= remaining) break;
+          above += sh.hist.cnt[d];
+        }
+        sh.bcast_u[0] = (uint32_t)d;
+        sh.bcast_u[1] = (uint32_t)(remaining - above);
+      }
+      __syncthreads();
+      prefix |= sh.bcast_u[0] << shift;
+      pmask |= 255u << shift;
+      remaining = sh.bcast_u[1];
+      __syncthreads();
+    }
+    kmin = prefix;
+  }
+
+  // ---- top-p: smallest key whose mass at or below it exceeds 1 - p ----------------------------
+  const float p = a.top_p ? a.top_p[row] : 1.0f;
+  uint32_t cut = kmin;
+  if (p < 1.0f) {
+    float zl = 0.f;
+    for (int64_t i = tid; i < V; i += kSampThreads) {
+      const float z = lg[i] / t;
+      if (ord_key(z) >= kmin) zl += expf(z - m);
+    }
+    const float zk = block_sum(zl, sh);
+    const double wscale = kMassScale / (double)zk;
+    const double tgt = (1.0 - (double)p) * kMassScale;
+    const unsigned long long target = tgt <= 0.0 ? 0ull : (unsigned long long)tgt;
+    uint32_t prefix = 0, pmask = 0;
+    unsigned long long below = 0;
+    bool found = true;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+      for (int b = tid; b < 256; b += kSampThreads) sh.hist.mass[b] = 0ull;
+      __syncthreads();
+      for (int64_t i = tid; i < V; i += kSampThreads) {
+        const float z = lg[i] / t;
+        const uint32_t key = ord_key(z);
+        if (key >= kmin && (key & pmask) == prefix) {
+          const unsigned long long w = (unsigned long long)((double)expf(z - m) * wscale);
+          atomicAdd(&sh.hist.mass[(key >> shift) & 255], w);
+        }
+      }
+      __syncthreads();
+      if (tid == 0) {
+        unsigned long long cum = below;
+        int d = 0;
+        bool hit = false;
+        for (; d < 256; ++d) {
+          if (cum + sh.hist.mass[d] > target) {
+            hit = true;
+            break;
+          }
+          cum += sh.hist.mass[d];
+        }
+        sh.bcast_u[0] = hit ? (uint32_t)d : 256u;
+        sh.bcast_ull = cum;
+      }
+      __syncthreads();
+      if (sh.bcast_u[0] == 256u) {  // rounding left no crossing: keep only the largest value
+        found = false;
+        break;
+      }
+      prefix |= sh.bcast_u[0] << shift;
+      pmask |= 255u << shift;
+      below = sh.bcast_ull;
+      __syncthreads();
+    }
+    cut = found ? max(prefix, kmin) : ord_key(m);
+  }
+
+  // ---- output over the kept set {ord_key(z) >= cut} -------------------------------------------
+  if (a.mode == SAMP_MASK) {
+    float* o = a.out + row * a.ldo;
+    for (int64_t i = tid; i < V; i += kSampThreads) {
+      const float z = lg[i] / t;
+      o[i] = ord_key(z) >= cut ? z : -INFINITY;
+    }
+    return;
+  }
+  float zl = 0.f;
+  for (int64_t i = tid; i < V; i += kSampThreads) {
+    const float z = lg[i] / t;
+    if (ord_key(z) >= cut) zl += expf(z - m);
+  }
+  const float zsum = block_sum(zl, sh);
+  if (a.mode == SAMP_PROBS) {
+    float* o = a.out + row * a.ldo;
+    for (int64_t i = tid; i < V; i += kSampThreads) {
+      const float z = lg[i] / t;
+      o[i] = ord_key(z) >= cut ? expf(z - m) / zsum : 0.f;
+    }
+    return;
+  }
+  const float* nz = a.noise + row * a.ldn;
+  float bv = -1.f;
+  int bi = 0x7fffffff;
+  for (int64_t i = tid; i < V; i += kSampThreads) {
+    const float z = lg[i] / t;
+    if (ord_key(z) < cut) continue;
+    const float s = (expf(z - m) / zsum) / fmaxf(nz[i], 1.17549435e-38f);  // noise clamped as the reference does
+    if (s > bv) {
+      bv = s;
+      bi = (int)i;
+    }
+  }
+  const int id = block_argmax(bv, bi, sh);
+  if (tid == 0) a.ids[row] = id;
+}
+
+static int sample_launch(SampArgs& a, int64_t rows, hipStream_t s, const char* what) {
+  if (rows == 0) return MSA_OK;
+  if (rows < 0 || rows > 0x7fffffff || a.vocab <= 0 || a.vocab > 0x7fffffff || !a.logits || a.ld < a.vocab)
+    return fail(MSA_ERR_INVALID, std::string(what) + ": bad shape or null logits");
+  hipLaunchKernelGGL(sample_rows_kernel, dim3((unsigned)rows), dim3(kSampThreads), 0, s, a);
+  return check_launch(what);
+}
+
+}  // namespace msa
+
+using namespace msa;
+
+extern "C" int msa_top_k_top_p_mask(const float* logits, int64_t ld, int64_t rows, int64_t vocab,
+                                    const int32_t* top_k, const float* top_p, float* out, int64_t ldo,
+                                    msa_stream_t stream) {
+  if (!out || ldo < vocab) return fail(MSA_ERR_INVALID, "msa_top_k_top_p_mask: bad out");
+  SampArgs a{};
+  a.logits = logits; a.ld = ld; a.vocab = vocab; a.top_k = top_k; a.top_p = top_p; a.out = out; a.ldo = ldo;
+  a.mode = SAMP_MASK;
+  return sample_launch(a, rows, (hipStream_t)stream, "msa_top_k_top_p_mask");
+}
+
+extern "C" int msa_sampling_probs(const float* logits, int64_t ld, int64_t rows, int64_t vocab, const float* temperature,
+                                  const int32_t* top_k, const float* top_p, float* probs, int64_t ldp,
+                                  msa_stream_t stream) {
+  if (!probs || ldp < vocab) return fail(MSA_ERR_INVALID, "msa_sampling_probs: bad probs");
+  SampArgs a{};
+  a.logits = logits; a.ld = ld; a.vocab = vocab; a.temperature = temperature; a.top_k = top_k; a.top_p = top_p;
+  a.out = probs; a.ldo = ldp; a.mode = SAMP_PROBS;
+  return sample_launch(a, rows, (hipStream_t)stream, "msa_sampling_probs");
+}
+
+extern "C" int msa_sample(const float* logits, int64_t ld, int64_t rows, int64_t vocab, const float* temperature,
+                          const int32_t* top_k, const float* top_p, const uint8_t* greedy, const float* noise,
+                          int64_t ldn, int64_t* out_ids, msa_stream_t stream) {
+  if (!out_ids || !noise || ldn < vocab) return fail(MSA_ERR_INVALID, "msa_sample: bad noise / out_ids");
+  SampArgs a{};
+  a.logits = logits; a.ld = ld; a.vocab = vocab; a.temperature = temperature; a.top_k = top_k; a.top_p = top_p;
+  a.greedy = greedy; a.noise = noise; a.ldn = ldn; a.ids = out_ids; a.mode = SAMP_SAMPLE;
+  return sample_launch(a, rows, (hipStream_t)stream, "msa_sample");
+}

@@ -474,3 +474,71 @@ def lm_head_argmax(
         vocab, _ptr(out), _ptr(ws), ws.numel() if ws is not None else 0, _stream(hidden),
     )
     return out
+
+
+# ---- sampling ---------------------------------------------------------------------------------------
+
+
+def _rows_f32(logits: Tensor, name: str) -> Tensor:
+    _check(logits.dtype == torch.float32 and logits.dim() == 2 and logits.stride(-1) == 1, f"{name}: float32 [R, V] logits")
+    return logits
+
+
+def _opt_param(t: Tensor | None, dtype: torch.dtype, rows: int, name: str) -> Tensor | None:
+    if t is None:
+        return None
+    _check(t.dtype == dtype and t.is_contiguous() and t.numel() == rows and t.is_cuda, f"{name}: [{rows}] {dtype}")
+    return t
+
+
+def top_k_top_p_mask(logits: Tensor, top_k: Tensor | None, top_p: Tensor | None) -> Tensor:
+    """logits where inside each row's top-k and top-p nucleus, -inf elsewhere (runner/sampler.py:12-27)."""
+    _on_gpu(logits)
+    _rows_f32(logits, "top_k_top_p_mask")
+    r, v = logits.shape
+    out = torch.empty_like(logits, memory_format=torch.contiguous_format)
+    _native.call("msa_top_k_top_p_mask", _ptr(logits), logits.stride(0), r, v,
+                 _ptr(_opt_param(top_k, torch.int32, r, "top_k")), _ptr(_opt_param(top_p, torch.float32, r, "top_p")),
+                 _ptr(out), out.stride(0), _stream(logits))
+    return out
+
+
+def sampling_probs(logits: Tensor, temperature: Tensor | None, top_k: Tensor | None, top_p: Tensor | None) -> Tensor:
+    """softmax(top-k / top-p of logits / temperature) per row (runner/sampler.py:30-40)."""
+    _on_gpu(logits)
+    _rows_f32(logits, "sampling_probs")
+    r, v = logits.shape
+    out = torch.empty_like(logits, memory_format=torch.contiguous_format)
+    _native.call("msa_sampling_probs", _ptr(logits), logits.stride(0), r, v,
+                 _ptr(_opt_param(temperature, torch.float32, r, "temperature")),
+                 _ptr(_opt_param(top_k, torch.int32, r, "top_k")), _ptr(_opt_param(top_p, torch.float32, r, "top_p")),
+                 _ptr(out), out.stride(0), _stream(logits))
+    return out
+
+
+def sample_ids(
+    logits: Tensor,
+    temperature: Tensor | None,
+    top_k: Tensor | None,
+    top_p: Tensor | None,
+    greedy: Tensor | None,
+    noise: Tensor | None,
+) -> Tensor:
+    """Token id per row: the greedy argmax where ``greedy``, else argmax(probs / noise) with the
+    probabilities of ``sampling_probs`` (runner/sampler.py:55-69). ``noise`` [R, V] float32 ~ Exp(1);
+    it may be None only when every row is greedy."""
+    _on_gpu(logits)
+    _rows_f32(logits, "sample_ids")
+    r, v = logits.shape
+    if noise is None:
+        _check(greedy is not None, "sample_ids: noise is required for sampled rows")
+        noise = logits  # never read: every row is greedy
+    _check(noise.dtype == torch.float32 and noise.dim() == 2 and noise.shape == (r, v) and noise.stride(-1) == 1,
+           "sample_ids: noise [R, V] float32")
+    out = torch.empty(r, dtype=torch.int64, device=logits.device)
+    _native.call("msa_sample", _ptr(logits), logits.stride(0), r, v,
+                 _ptr(_opt_param(temperature, torch.float32, r, "temperature")),
+                 _ptr(_opt_param(top_k, torch.int32, r, "top_k")), _ptr(_opt_param(top_p, torch.float32, r, "top_p")),
+                 _ptr(_opt_param(greedy, torch.uint8, r, "greedy")), _ptr(noise), noise.stride(0), _ptr(out),
+                 _stream(logits))
+    return out

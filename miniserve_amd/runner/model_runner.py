@@ -7,7 +7,9 @@ sequence's new tokens into one batch with per-token positions and slots (model_r
 computes logits only for rows that are sampled and syncs once per step (model_runner.py:207-239).
 The engine, scheduler and block manager stay with the caller: a ``ScheduledChunk`` carries what the
 runner reads from the reference's ``ScheduledSeq`` (token ids, tokens already computed, tokens
-scheduled now, block table).
+scheduled now, block table) and, for a sampled request, its ``SamplingParams`` and generator.
+Greedy steps sample inside the fused LM head + argmax; steps with temperature / top-k / top-p rows
+compute the sampled rows' logits and run the sampling kernel (runner/sampler.py).
 
 Pure decode steps (every sequence schedules one token) run as a captured HIP graph per batch size
 (``use_graphs``): the forward, the LM head and the greedy argmax replay with one launch; the
@@ -19,6 +21,7 @@ static device buffers from one pinned host buffer first. This is the reference's
 from __future__ import annotations
 
 from dataclasses import dataclass
+from typing import Any
 
 import numpy as np
 import torch
@@ -26,6 +29,7 @@ from torch import Tensor
 
 from miniserve_amd.attention.backends import AttentionMetadata, DecodePlan, SeqChunk, build_attention_metadata
 from miniserve_amd.model.qwen3 import Qwen3ForCausalLM
+from miniserve_amd.runner.sampler import sample
 from miniserve_amd.utils import to_device
 
 
@@ -35,6 +39,12 @@ class ScheduledChunk:
     num_computed: int
     num_new: int
     block_table: list[int]
+    params: Any = None  # the request's SamplingParams (temperature, top_k, top_p, greedy); None: greedy
+    generator: torch.Generator | None = None  # a seeded request's generator (model_runner.py:_generator)
+
+    @property
+    def greedy(self) -> bool:
+        return self.params is None or bool(self.params.greedy)
 
 
 @dataclass
@@ -44,6 +54,17 @@ class StepInputs:
     attn: AttentionMetadata
     logits_rows: Tensor
     sample_idx: list[int]
+
+
+@dataclass(frozen=True)
+class _Greedy:
+    temperature: float = 0.0
+    top_k: int = -1
+    top_p: float = 1.0
+    greedy: bool = True
+
+
+_GREEDY = _Greedy()
 
 
 class CapturedDecode:
@@ -180,6 +201,7 @@ class ModelRunner:
     def _graphable(self, scheduled: list[ScheduledChunk]) -> bool:
         return all(
             s.num_new == 1 and s.num_computed + 1 == len(s.token_ids) and s.num_computed < self.max_model_len
+            and s.greedy
             for s in scheduled
         )
 
@@ -209,7 +231,13 @@ class ModelRunner:
         if inp.logits_rows.numel() == 0:
             self.model(inp.input_ids, inp.positions, self.kv_caches, inp.attn)
             return results
-        tokens = self.forward_greedy(inp).tolist()  # the one device -> host sync
+        sampled = [scheduled[i] for i in inp.sample_idx]
+        if all(s.greedy for s in sampled):
+            tokens = self.forward_greedy(inp).tolist()  # the one device -> host sync
+        else:  # temperature / top-k / top-p rows: logits of the sampled rows, then the sampling kernel
+            logits = self.forward_logits(inp)
+            params = [s.params if s.params is not None else _GREEDY for s in sampled]
+            tokens = sample(logits, params, [s.generator for s in sampled]).tolist()
         for j, idx in enumerate(inp.sample_idx):
             results[idx] = [tokens[j]]
         return results

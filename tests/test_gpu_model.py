@@ -230,6 +230,49 @@ def test_captured_decode_matches_eager(batch):
         seqs = [ScheduledChunk(s.token_ids + [eager[i]], len(s.token_ids), 1, s.block_table) for i, s in enumerate(seqs)]
 
 
+def test_runner_samples_with_request_settings():
+    """ModelRunner.execute with per-request sampling (model_runner.py:207-230): top_k = 1 and a
+    tiny top_p give the greedy ids, greedy rows are untouched by sampled neighbours, a seeded
+    request repeats its token from a fresh generator, and sampled ids stay in the vocabulary."""
+    from dataclasses import dataclass
+
+    @dataclass
+    class Params:
+        temperature: float = 1.0
+        top_p: float = 1.0
+        top_k: int = -1
+
+        @property
+        def greedy(self) -> bool:
+            return self.temperature < 1e-5
+
+    weights = workloads.random_weights(SMALL, seed=21, norm_jitter=0.1)
+    model = workloads.build_model(SMALL, weights, DEV, 512)
+    quantize_int8_(model)
+    runner = ModelRunner(model, DEV, use_graphs=True, max_model_len=512)
+    runner.allocate_kv_cache(64)
+    rng = random.Random(22)
+    prompts = [[rng.randrange(1024) for _ in range(n)] for n in (9, 30, 17, 4)]
+    tables = [[8 * i + j for j in range(8)] for i in range(4)]
+
+    def step(params, gens=None):
+        gens = gens or [None] * 4
+        return [r[0] for r in runner.execute([ScheduledChunk(p, 0, len(p), t, params=q, generator=g)
+                                              for p, t, q, g in zip(prompts, tables, params, gens, strict=True)])]
+
+    greedy = step([None] * 4)
+    assert step([Params(top_k=1), Params(top_p=1e-6), None, Params(temperature=0.0)]) == greedy
+    mixed = step([None, Params(temperature=1.2, top_k=50, top_p=0.9), None, Params(temperature=0.7)])
+    assert mixed[0] == greedy[0] and mixed[2] == greedy[2]
+    assert all(0 <= t < SMALL["vocab_size"] for t in mixed)
+
+    def seeded():
+        return [torch.Generator(device=DEV).manual_seed(5) for _ in range(4)]
+
+    params = [Params(temperature=1.0)] * 4
+    assert step(params, seeded()) == step(params, seeded())
+
+
 def test_small_model_long_prefill_gemm_path():
     """A 300-token prompt (above the token-split pipeline's 256-token limit) runs the GEMM
     layer pipeline and the prenormed LM-head path; logits and greedy ids match the oracle."""

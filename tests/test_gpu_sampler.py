@@ -1,0 +1,152 @@
+"""GPU parity of the sampling kernel (top-k / top-p without a sort, temperature, the exponential
+race) against the sampling oracle and a float64 brute force on the same logits and noise.
+
+Bars: kept masks identical to the float64 brute force (and the oracle) on every row whose top-p
+cut is decidable (no cumulative probability within 1e-5 of 1 - p); on the other rows (a cut in the
+dense tail of a 151,936-entry vocabulary, where the reference's own float32 cumsum decides by
+rounding) only tokens within 1e-5 of the cut may differ; probabilities within rel-L2 1e-5 of the
+oracle's on decidable rows; sampled ids equal to the oracle's given the same noise wherever the
+best two scores differ by more than 1e-4 relative; the reference's own unit cases exactly.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+import pytest
+import torch
+from helpers import rel_l2
+from test_oracle_sampler import CHI2_DF4_P001, brute_force_cut, brute_force_mask, chi_square
+
+from miniserve_amd import kernels
+from miniserve_amd.runner import sampler as hs
+from oracle import sampler as osm
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+@dataclass
+class Params:
+    temperature: float = 1.0
+    top_p: float = 1.0
+    top_k: int = -1
+
+    @property
+    def greedy(self) -> bool:
+        return self.temperature < 1e-5
+
+
+def _case(rows, vocab, seed):
+    g = torch.Generator().manual_seed(seed)
+    logits = torch.randn(rows, vocab, generator=g) * 3
+    k = torch.randint(1, 200, (rows,), generator=g).to(torch.int32)
+    k[::4] = vocab  # every fourth row: no top-k
+    p = (torch.rand(rows, generator=g) * 0.9 + 0.05).float()
+    p[1::4] = 1.0  # no top-p
+    return logits, k, p
+
+
+def test_reference_unit_cases():
+    logits = torch.tensor([[1.0, 4.0, 3.0, 2.0, 0.0]], device=DEV)
+    kept = hs.apply_top_k_top_p(logits, torch.tensor([2]), torch.tensor([1.0])) > float("-inf")
+    assert kept.cpu().tolist() == [[False, True, True, False, False]]
+    kept = hs.apply_top_k_top_p(logits, torch.tensor([5]), torch.tensor([0.8])) > float("-inf")
+    assert kept.cpu().tolist() == [[False, True, True, False, False]]
+    x = torch.randn(6, 50, generator=torch.Generator().manual_seed(1)).to(DEV)
+    assert torch.equal(hs.sample(x, [Params(temperature=0)] * 6, [None] * 6), x.argmax(-1))
+    y = torch.randn(4, 100, generator=torch.Generator().manual_seed(2)).to(DEV)
+    params = [Params(top_k=1), Params(top_p=1e-6)] * 2
+    assert torch.equal(hs.sample(y, params, [None] * 4), y.argmax(-1))
+
+
+@pytest.mark.parametrize("rows,vocab", [(64, 151936), (33, 5000), (8, 64)])
+def test_masks_match_float64_brute_force(rows, vocab):
+    logits, k, p = _case(rows, vocab, seed=vocab)
+    got = kernels.top_k_top_p_mask(logits.to(DEV), k.to(DEV), p.to(DEV)).cpu()
+    ref = osm.apply_top_k_top_p(logits, k.long(), p)
+    exact = 0
+    for r in range(rows):
+        kept = got[r] > float("-inf")
+        assert torch.equal(got[r][kept], logits[r][kept])  # kept values untouched
+        mask, boundary = brute_force_cut(logits[r].double().numpy(), int(k[r]), float(p[r]), tol=1e-5)
+        if not boundary.any():  # decidable: identical to the brute force and to the oracle
+            assert np.array_equal(kept.numpy(), mask), r
+            assert torch.equal(kept, ref[r] > float("-inf")), r
+            exact += 1
+        else:  # a cut inside the dense tail: only tokens at the cut may fall either way
+            differ = kept.numpy() != mask
+            assert not (differ & ~boundary).any(), (r, int(differ.sum()))
+    assert exact >= rows // 2
+
+
+def test_probs_match_the_oracle():
+    rows, vocab = 48, 151936
+    logits, k, p = _case(rows, vocab, seed=3)
+    temps = (torch.rand(rows, generator=torch.Generator().manual_seed(4)) * 1.5 + 0.2).float()
+    got = kernels.sampling_probs(logits.to(DEV), temps.to(DEV), k.to(DEV), p.to(DEV)).cpu()
+    ref = osm.compute_probs(logits, temps, k.long(), p)
+    for r in range(rows):
+        z = (logits[r] / temps[r]).double().numpy()
+        _, ok = brute_force_mask(z, int(k[r]), float(p[r]))
+        if ok:
+            assert rel_l2(got[r], ref[r]) < 1e-5, r
+    assert torch.allclose(got.sum(-1), torch.ones(rows), atol=1e-5)
+
+
+def test_sampled_ids_match_the_oracle_with_the_same_noise():
+    rows, vocab = 64, 151936
+    logits, k, p = _case(rows, vocab, seed=5)
+    temps = torch.full((rows,), 0.8)
+    greedy = torch.zeros(rows, dtype=torch.bool)
+    greedy[::8] = True
+    noise = torch.empty(rows, vocab).exponential_(generator=torch.Generator().manual_seed(6))
+    got = kernels.sample_ids(logits.to(DEV), temps.to(DEV), k.to(DEV), p.to(DEV), greedy.to(torch.uint8).to(DEV),
+                             noise.to(DEV)).cpu()
+    ref = osm.sample(logits, temps, k.long(), p, greedy, noise)
+    probs = osm.compute_probs(logits, temps, k.long(), p)
+    checked = 0
+    for r in range(rows):
+        z = (logits[r] / temps[r]).double().numpy()
+        _, ok = brute_force_mask(z, int(k[r]), float(p[r]))
+        s = (probs[r] / noise[r]).double()
+        top2 = s.topk(2).values
+        if greedy[r] or (ok and float(top2[0] - top2[1]) > 1e-4 * float(top2[0])):
+            assert int(got[r]) == int(ref[r]), r
+            checked += 1
+    assert checked >= rows * 3 // 4
+
+
+def test_sampling_distribution_and_seeded_rows():
+    rows = 100_000
+    logits = torch.tensor([[0.5, 1.5, -1.0, 0.0, 1.0]], device=DEV).repeat(rows, 1)
+    torch.manual_seed(0)
+    tokens = hs.sample(logits, [Params(temperature=1.0)] * rows, [None] * rows)
+    counts = torch.bincount(tokens.cpu(), minlength=5).double()
+    assert chi_square(counts, logits[0].cpu().double().softmax(-1)) < CHI2_DF4_P001
+    x = torch.randn(3, 1000, generator=torch.Generator().manual_seed(7)).to(DEV)
+    params = [Params(temperature=1.0)] * 3
+
+    def gens():
+        return [torch.Generator(device=DEV).manual_seed(7) for _ in range(3)]
+
+    assert torch.equal(hs.sample(x, params, gens()), hs.sample(x, params, gens()))
+
+
+def test_edge_rows():
+    """-inf entries, every value equal with top-k (the ties at the k-th value are all kept, as
+    `sorted < kth` keeps them), k = vocab - 1, p just below 1."""
+    vocab = 1000
+    x = torch.randn(4, vocab, generator=torch.Generator().manual_seed(8))
+    x[0, ::3] = float("-inf")
+    x[1] = 0.25
+    k = torch.tensor([10, 3, vocab - 1, vocab], dtype=torch.int32)
+    p = torch.tensor([1.0, 1.0, 1.0, 0.999])
+    got = kernels.top_k_top_p_mask(x.to(DEV), k.to(DEV), p.to(DEV)).cpu()
+    ref = osm.apply_top_k_top_p(x, k.long(), p)
+    assert torch.equal(got[0] > float("-inf"), ref[0] > float("-inf"))
+    assert bool((got[1] > float("-inf")).all()) and bool((ref[1] > float("-inf")).all())
+    assert torch.equal(got[2] > float("-inf"), ref[2] > float("-inf"))
+    mask, ok = brute_force_mask(x[3].double().numpy(), vocab, 0.999)
+    assert not ok or np.array_equal((got[3] > float("-inf")).numpy(), mask)
