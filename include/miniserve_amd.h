@@ -235,6 +235,24 @@ int msa_sample(const float* logits, int64_t ld, int64_t rows, int64_t vocab, con
                const int32_t* top_k, const float* top_p, const uint8_t* greedy, const float* noise, int64_t ldn,
                int64_t* out_ids, msa_stream_t stream);
 
+/* ---- speculative-decoding verification (spec/rejection.py) ----------------------------------- */
+
+/* verify_greedy (spec/rejection.py:27-40) from the target's per-position argmax target_ids
+ * [batch, k + 1] (int64; msa_sample with every row greedy computes them from logits): accepted[i] =
+ * leading run of drafts[i, j] == target_ids[i, j] over j < num_drafts[i]; next_token[i] =
+ * target_ids[i, accepted[i]]. drafts [batch, k] int64. */
+int msa_verify_greedy(const int64_t* target_ids, int64_t batch, int64_t k, const int64_t* drafts,
+                      const int64_t* num_drafts, int64_t* accepted, int64_t* next_token, msa_stream_t stream);
+
+/* verify_sampled (spec/rejection.py:43-79): target_probs [batch, k + 1, vocab], drafts [batch, k],
+ * num_drafts [batch], draft_probs [batch, k, vocab] or NULL (a deterministic proposer), uniform
+ * [batch, k] ~ U(0, 1), noise [batch, vocab] ~ Exp(1); float32 tensors contiguous. Accepts draft j
+ * while uniform < min(1, p_j(d_j) / q_j(d_j)); next_token samples normalize(max(0, p_a - q_a)) after
+ * a rejection (p_a with the draft zeroed when q is NULL), else p_a, as argmax(dist / noise). k >= 1. */
+int msa_verify_sampled(const float* target_probs, int64_t batch, int64_t k, int64_t vocab, const int64_t* drafts,
+                       const int64_t* num_drafts, const float* draft_probs, const float* uniform, const float* noise,
+                       int64_t* accepted, int64_t* next_token, msa_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -84,6 +84,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p,
          c_void_p],
     ),
+    "msa_verify_greedy": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "msa_verify_sampled": (
+        c_int,
+        [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+         c_void_p],
+    ),
     "msa_paged_attention_decode_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int]),
     "msa_paged_attention_decode": (
         c_int,

@@ -269,6 +269,88 @@ __global__ __launch_bounds__(kSampThreads) void sample_rows_kernel(SampArgs a) {
   if (tid == 0) a.ids[row] = id;
 }
 
+// ---- speculative-decoding verification (spec/rejection.py) ------------------------------------
+
+// Greedy verification from the target's own picks (spec/rejection.py:27-40): accepted = length of
+// the leading run of drafts equal to the target's argmax at their position (among the real ones),
+// next = the target's pick right after the run (a correction, or the bonus token).
+__global__ void verify_greedy_kernel(const int64_t* __restrict__ target_ids, int k, const int64_t* __restrict__ drafts,
+                                     const int64_t* __restrict__ num_drafts, int b, int64_t* __restrict__ accepted,
+                                     int64_t* __restrict__ next_token) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= b) return;
+  const int64_t* tgt = target_ids + (int64_t)i * (k + 1);
+  const int64_t* dr = drafts + (int64_t)i * k;
+  const int64_t n = num_drafts[i];
+  int a = 0;
+  while (a < k && a < n && tgt[a] == dr[a]) ++a;
+  accepted[i] = a;
+  next_token[i] = tgt[a];
+}
+
+// Rejection sampling (spec/rejection.py:43-79), one workgroup per sequence. p_i(d_i) / q_i(d_i)
+// (q = 1 for a deterministic proposer) against uniform[i], the leading accepted run a, then a
+// token from normalize(max(0, p_a - q_a)) (p_a with the rejected draft zeroed when q is one-hot)
+// after a rejection, or from p_a itself when every real draft was accepted (the bonus token);
+// normalize falls back to p_a when the residual is empty. The token is the first argmax of
+// dist / noise.
+__global__ __launch_bounds__(kSampThreads) void verify_sampled_kernel(
+    const float* __restrict__ target_probs, int k, int64_t vocab, const int64_t* __restrict__ drafts,
+    const int64_t* __restrict__ num_drafts, const float* __restrict__ draft_probs, const float* __restrict__ uniform,
+    const float* __restrict__ noise, int64_t* __restrict__ accepted, int64_t* __restrict__ next_token) {
+  __shared__ SampShared sh;
+  __shared__ int s_acc;
+  const int64_t b = blockIdx.x;
+  const float* tp = target_probs + b * (int64_t)(k + 1) * vocab;
+  const float* dp = draft_probs ? draft_probs + b * (int64_t)k * vocab : nullptr;
+  const int64_t* dr = drafts + b * k;
+  if (threadIdx.x == 0) {
+    const int64_t n = num_drafts[b];
+    int a = 0;
+    while (a < k) {
+      int64_t d = dr[a];
+      d = d < 0 ? 0 : (d >= vocab ? vocab - 1 : d);  // memory safety only: draft ids are vocabulary ids
+      const float pd = tp[(int64_t)a * vocab + d];
+      const float ratio = dp ? pd / fmaxf(dp[(int64_t)a * vocab + d], 1e-20f) : pd;
+      if (!(a < n && uniform[b * k + a] < fminf(ratio, 1.0f))) break;
+      ++a;
+    }
+    s_acc = a;
+  }
+  __syncthreads();
+  const int a = s_acc;
+  const bool rejected = a < num_drafts[b];
+  const int at = min(a, k - 1);
+  const float* prow = tp + (int64_t)a * vocab;
+  const float* qrow = dp ? dp + (int64_t)at * vocab : nullptr;
+  const int64_t drop = k > 0 ? dr[at] : -1;
+  auto dist = [&](int64_t i) -> float {
+    const float pv = prow[i];
+    if (!rejected) return pv;
+    if (qrow) return fmaxf(pv - qrow[i], 0.f);
+    return i == drop ? 0.f : pv;
+  };
+  float tl = 0.f;
+  for (int64_t i = threadIdx.x; i < vocab; i += kSampThreads) tl += dist(i);
+  const float total = block_sum(tl, sh);
+  const float* nz = noise + b * vocab;
+  float bv = -1.f;
+  int bi = 0x7fffffff;
+  for (int64_t i = threadIdx.x; i < vocab; i += kSampThreads) {
+    const float dv = total > 0.f ? dist(i) / fmaxf(total, 1e-20f) : prow[i];
+    const float sc = dv / fmaxf(nz[i], 1.17549435e-38f);
+    if (sc > bv) {
+      bv = sc;
+      bi = (int)i;
+    }
+  }
+  const int id = block_argmax(bv, bi, sh);
+  if (threadIdx.x == 0) {
+    accepted[b] = a;
+    next_token[b] = id;
+  }
+}
+
 static int sample_launch(SampArgs& a, int64_t rows, hipStream_t s, const char* what) {
   if (rows == 0) return MSA_OK;
   if (rows < 0 || rows > 0x7fffffff || a.vocab <= 0 || a.vocab > 0x7fffffff || !a.logits || a.ld < a.vocab)
@@ -309,4 +391,30 @@ extern "C" int msa_sample(const float* logits, int64_t ld, int64_t rows, int64_t
   a.logits = logits; a.ld = ld; a.vocab = vocab; a.temperature = temperature; a.top_k = top_k; a.top_p = top_p;
   a.greedy = greedy; a.noise = noise; a.ldn = ldn; a.ids = out_ids; a.mode = SAMP_SAMPLE;
   return sample_launch(a, rows, (hipStream_t)stream, "msa_sample");
+}
+
+extern "C" int msa_verify_greedy(const int64_t* target_ids, int64_t batch, int64_t k, const int64_t* drafts,
+                                 const int64_t* num_drafts, int64_t* accepted, int64_t* next_token,
+                                 msa_stream_t stream) {
+  if (batch == 0) return MSA_OK;
+  if (!target_ids || !drafts || !num_drafts || !accepted || !next_token)
+    return fail(MSA_ERR_INVALID, "msa_verify_greedy: null pointer");
+  if (batch < 0 || batch > 0x7fffffff || k < 0 || k > 0x7fffffff) return fail(MSA_ERR_INVALID, "msa_verify_greedy: bad shape");
+  hipLaunchKernelGGL(verify_greedy_kernel, dim3((unsigned)((batch + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                     target_ids, (int)k, drafts, num_drafts, (int)batch, accepted, next_token);
+  return check_launch("msa_verify_greedy");
+}
+
+extern "C" int msa_verify_sampled(const float* target_probs, int64_t batch, int64_t k, int64_t vocab,
+                                  const int64_t* drafts, const int64_t* num_drafts, const float* draft_probs,
+                                  const float* uniform, const float* noise, int64_t* accepted, int64_t* next_token,
+                                  msa_stream_t stream) {
+  if (batch == 0) return MSA_OK;
+  if (!target_probs || !drafts || !num_drafts || !uniform || !noise || !accepted || !next_token)
+    return fail(MSA_ERR_INVALID, "msa_verify_sampled: null pointer");
+  if (batch < 0 || batch > 0x7fffffff || k < 1 || k > 0x7fffffff || vocab <= 0 || vocab > 0x7fffffff)
+    return fail(MSA_ERR_INVALID, "msa_verify_sampled: bad shape (k >= 1)");
+  hipLaunchKernelGGL(verify_sampled_kernel, dim3((unsigned)batch), dim3(kSampThreads), 0, (hipStream_t)stream,
+                     target_probs, (int)k, vocab, drafts, num_drafts, draft_probs, uniform, noise, accepted, next_token);
+  return check_launch("msa_verify_sampled");
 }

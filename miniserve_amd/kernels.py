@@ -542,3 +542,46 @@ def sample_ids(
                  _ptr(_opt_param(greedy, torch.uint8, r, "greedy")), _ptr(noise), noise.stride(0), _ptr(out),
                  _stream(logits))
     return out
+
+
+# ---- speculative-decoding verification --------------------------------------------------------------
+
+
+def _i64(t: Tensor, shape: tuple[int, ...], name: str) -> Tensor:
+    _check(t.is_cuda and t.dtype == torch.int64 and tuple(t.shape) == shape, f"{name}: int64 {list(shape)}")
+    return t.contiguous()
+
+
+def verify_greedy_ids(target_ids: Tensor, drafts: Tensor, num_drafts: Tensor) -> tuple[Tensor, Tensor]:
+    """(accepted [B], next_token [B]) from the target's argmax ids [B, K+1] (spec/rejection.py:27-40)."""
+    _on_gpu(target_ids, drafts, num_drafts)
+    b, k1 = target_ids.shape
+    ids = _i64(target_ids, (b, k1), "target_ids")
+    dr = _i64(drafts, (b, k1 - 1), "drafts")
+    nd = _i64(num_drafts, (b,), "num_drafts")
+    accepted = torch.empty(b, dtype=torch.int64, device=ids.device)
+    nxt = torch.empty_like(accepted)
+    _native.call("msa_verify_greedy", _ptr(ids), b, k1 - 1, _ptr(dr), _ptr(nd), _ptr(accepted), _ptr(nxt), _stream(ids))
+    return accepted, nxt
+
+
+def verify_sampled(
+    target_probs: Tensor, drafts: Tensor, num_drafts: Tensor, draft_probs: Tensor | None, uniform: Tensor, noise: Tensor
+) -> tuple[Tensor, Tensor]:
+    """(accepted [B], next_token [B]) by rejection sampling (spec/rejection.py:43-79)."""
+    _on_gpu(target_probs, drafts, num_drafts, uniform, noise)
+    b, k1, v = target_probs.shape
+    k = k1 - 1
+    _check(k >= 1, "verify_sampled: at least one draft position")
+    tp = target_probs.float().contiguous()
+    dp = None
+    if draft_probs is not None:
+        _check(tuple(draft_probs.shape) == (b, k, v), "verify_sampled: draft_probs [B, K, V]")
+        dp = draft_probs.float().contiguous()
+    _check(tuple(uniform.shape) == (b, k) and tuple(noise.shape) == (b, v), "verify_sampled: uniform [B, K], noise [B, V]")
+    accepted = torch.empty(b, dtype=torch.int64, device=tp.device)
+    nxt = torch.empty_like(accepted)
+    _native.call("msa_verify_sampled", _ptr(tp), b, k, v, _ptr(_i64(drafts, (b, k), "drafts")),
+                 _ptr(_i64(num_drafts, (b,), "num_drafts")), _ptr(dp), _ptr(uniform.float().contiguous()),
+                 _ptr(noise.float().contiguous()), _ptr(accepted), _ptr(nxt), _stream(tp))
+    return accepted, nxt
