@@ -103,13 +103,20 @@ __global__ __launch_bounds__(64 * W) void paged_decode_kernel(DecodeArgs a) {
   __shared__ float s_acc[W][G][kHeadDim];
   __shared__ float s_ml[W][G][2];
   const int kvh = blockIdx.x, split = blockIdx.y, seq = blockIdx.z;
-  const int ctx = decode_context(a, seq);
   const int start = split * a.part_tokens;
-  if (start >= ctx) return;  // the reduce kernel merges only splits that hold keys
-  const int end = min(ctx, start + a.part_tokens);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int rp = lane >> 3, dg = lane & 7;
+  const int32_t* btr = a.bt + (int64_t)seq * a.max_blocks;
+  const int64_t tok_stride = (int64_t)a.kv_heads * kHeadDim;
+  const int64_t lane_off = (int64_t)(2 * rp) * tok_stride + (int64_t)kvh * kHeadDim + 8 * dg;
+  // Table entries of this wavefront's first two blocks are read with the context length, not after
+  // it: every index below max_blocks lies inside the table row, and a block past the context
+  // (a padding entry) is loaded but never used.
+  const int bfirst = start / kBlock + wave;
+  const int ph0 = bfirst < a.max_blocks ? btr[bfirst] : 0;
+  const int ph1 = bfirst + W < a.max_blocks ? btr[bfirst + W] : 0;
   const int64_t qrow = a.qrows[seq];
+  const int ctx = decode_context(a, seq);
 
   // q of this lane's 16 dims for each head of the group, as bf16 pairs
   uint32_t qv[G][8];
@@ -129,18 +136,10 @@ __global__ __launch_bounds__(64 * W) void paged_decode_kernel(DecodeArgs a) {
     for (int e = 0; e < 16; ++e) acc[h][e] = 0.f;
   }
 
-  const int b1 = (end + kBlock - 1) / kBlock;
-  const int32_t* btr = a.bt + (int64_t)seq * a.max_blocks;
-  const int64_t tok_stride = (int64_t)a.kv_heads * kHeadDim;
-  const int64_t lane_off = (int64_t)(2 * rp) * tok_stride + (int64_t)kvh * kHeadDim + 8 * dg;
-  auto block_ptr = [&](int b) -> int64_t {
-    int phys = btr[b];
+  // [row rr][half]: rows 2rp + rr, dims 8dg.. (half 0) and 64 + 8dg.. (half 1) of physical block phys
+  auto load_block = [&](int phys, uint4 (&kr)[2][2], uint4 (&vr)[2][2]) {
     phys = ((uint32_t)phys < (uint64_t)a.num_blocks) ? phys : 0;  // out-of-range table entries read block 0
-    return (int64_t)phys * kBlock * tok_stride + lane_off;
-  };
-  // [row rr][half]: rows 2rp + rr, dims 8dg.. (half 0) and 64 + 8dg.. (half 1)
-  auto load_block = [&](int b, uint4 (&kr)[2][2], uint4 (&vr)[2][2]) {
-    const int64_t base = block_ptr(b);
+    const int64_t base = (int64_t)phys * kBlock * tok_stride + lane_off;
 #pragma unroll
     for (int rr = 0; rr < 2; ++rr)
 #pragma unroll
@@ -149,6 +148,11 @@ __global__ __launch_bounds__(64 * W) void paged_decode_kernel(DecodeArgs a) {
         vr[rr][hf] = *(const uint4*)(a.vc + base + rr * tok_stride + 64 * hf);
       }
   };
+  uint4 ka[2][2], va[2][2], kb[2][2], vb[2][2];
+  if (bfirst < a.max_blocks) load_block(ph0, ka, va);  // before the context length is known
+  if (start >= ctx) return;  // the reduce kernel merges only splits that hold keys
+  const int end = min(ctx, start + a.part_tokens);
+  const int b1 = (end + kBlock - 1) / kBlock;
 
   // One block of q.k, online softmax and p.v on K/V registers kr, vr (wave-uniform block index).
   auto process = [&](int blk, const uint4 (&kr)[2][2], uint4 (&vr)[2][2]) {
@@ -206,18 +210,22 @@ __global__ __launch_bounds__(64 * W) void paged_decode_kernel(DecodeArgs a) {
     }
   };
 
-  // Two register buffers in turn: the next block's loads are in flight while one is processed.
-  int b = start / kBlock + wave;
-  uint4 ka[2][2], va[2][2], kb[2][2], vb[2][2];
-  if (b < b1) load_block(b, ka, va);
+  // Two register buffers in turn: the next block's loads are in flight while one is processed,
+  // and the table entry of the block after it is read one step ahead.
+  int b = bfirst;
+  int ph_next = ph1;  // table entry of block b + W
   while (b < b1) {
-    if (b + W < b1) load_block(b + W, kb, vb);
+    const int ph_a = b + 2 * W < a.max_blocks ? btr[b + 2 * W] : 0;
+    if (b + W < b1) load_block(ph_next, kb, vb);
     process(b, ka, va);
     b += W;
+    ph_next = ph_a;
     if (b >= b1) break;
-    if (b + W < b1) load_block(b + W, ka, va);
+    const int ph_b = b + 2 * W < a.max_blocks ? btr[b + 2 * W] : 0;
+    if (b + W < b1) load_block(ph_next, ka, va);
     process(b, kb, vb);
     b += W;
+    ph_next = ph_b;
   }
   // Merge the row pairs of the wavefront (lanes dg, dg + 8, ...), then the wavefronts through LDS.
   // acc[h][e]: dim 8dg + e for e < 8, 64 + 8dg + (e - 8) for e >= 8.
