@@ -291,9 +291,12 @@ __global__ __launch_bounds__(kHeadDim) void paged_decode_reduce_kernel(DecodeArg
 
 // ---------------------------------------------------------------------------------------------
 
-constexpr int kKeyTile = 32;
+constexpr int kKeyTile = 64;             // keys per LDS tile
 constexpr int kKsStride = kHeadDim + 8;  // bf16 elements per K row in LDS
 constexpr int kVtStride = kKeyTile + 4;  // bf16 elements per transposed V row in LDS
+constexpr int kKsTile = kKeyTile * kKsStride;
+constexpr int kVtTile = kHeadDim * kVtStride;
+constexpr size_t kPrefillLds = (size_t)2 * (kKsTile + kVtTile) * 2;  // two buffers of K and V^T
 
 struct PrefillArgs {
   const uint16_t* q;
@@ -321,8 +324,9 @@ template <int G>
 __global__ __launch_bounds__(256) void paged_prefill_kernel(PrefillArgs a) {
   constexpr int kSub = 4 / G;       // 16-token query sub-tiles per workgroup
   constexpr int kQTok = 16 * kSub;  // query tokens per workgroup
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[kKeyTile * kKsStride];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[kHeadDim * kVtStride];
+  extern __shared__ __attribute__((aligned(16))) uint16_t psm[];
+  uint16_t* Ks = psm;                // [2][kKeyTile][kKsStride]
+  uint16_t* Vt = psm + 2 * kKsTile;  // [2][kHeadDim][kVtStride]
 
   const int wi = blockIdx.x, kvh = blockIdx.y;
   const int seq = a.work[2 * wi], tstart = a.work[2 * wi + 1];
@@ -350,23 +354,35 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(PrefillArgs a) {
   const int32_t* btr = a.bt + (int64_t)seq * a.max_blocks;
   const int64_t tok_stride = (int64_t)a.kv_heads * kHeadDim;
 
-  // Loader role: key pair la (keys 2la, 2la+1 of the tile), 8-wide dim chunk lb.
-  const int la = lane & 15, lb = wave * 4 + (lane >> 4);
-  uint4 kr[2], vr[2];
+  // Loader role: keys 2la and 2la + 1 of the tile, 8-wide dim chunks lb and lb + 8.
+  const int la = threadIdx.x & 31, lb = threadIdx.x >> 5;
+  uint4 kr[2][2], vr[2][2];  // [key rr][chunk cc]
   auto load_tile = [&](int tile) {
 #pragma unroll
     for (int rr = 0; rr < 2; ++rr) {
       const int key = tile * kKeyTile + 2 * la + rr;
-      if (key < kend && key / kBlock < a.max_blocks) {
-        int phys = btr[key / kBlock];
-        phys = ((uint32_t)phys < (uint64_t)a.num_blocks) ? phys : 0;
-        const int64_t off = ((int64_t)phys * kBlock + key % kBlock) * tok_stride + (int64_t)kvh * kHeadDim + 8 * lb;
-        kr[rr] = *(const uint4*)(a.kc + off);
-        vr[rr] = *(const uint4*)(a.vc + off);
-      } else {
-        kr[rr] = uint4{0, 0, 0, 0};
-        vr[rr] = uint4{0, 0, 0, 0};
+      const bool ok = key < kend && key / kBlock < a.max_blocks;
+      int phys = ok ? btr[key / kBlock] : 0;
+      phys = ((uint32_t)phys < (uint64_t)a.num_blocks) ? phys : 0;
+      const int64_t off = ((int64_t)phys * kBlock + key % kBlock) * tok_stride + (int64_t)kvh * kHeadDim + 8 * lb;
+#pragma unroll
+      for (int cc = 0; cc < 2; ++cc) {
+        kr[rr][cc] = ok ? *(const uint4*)(a.kc + off + 64 * cc) : uint4{0, 0, 0, 0};
+        vr[rr][cc] = ok ? *(const uint4*)(a.vc + off + 64 * cc) : uint4{0, 0, 0, 0};
       }
+    }
+  };
+  auto store_tile = [&](int buf) {
+    uint16_t* K = Ks + buf * kKsTile;
+    uint16_t* V = Vt + buf * kVtTile;
+#pragma unroll
+    for (int cc = 0; cc < 2; ++cc) {
+#pragma unroll
+      for (int rr = 0; rr < 2; ++rr) *(uint4*)&K[(2 * la + rr) * kKsStride + 8 * lb + 64 * cc] = kr[rr][cc];
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        *(uint32_t*)&V[(8 * lb + 64 * cc + e) * kVtStride + 2 * la] =
+            (uint32_t)elem16(vr[0][cc], e) | ((uint32_t)elem16(vr[1][cc], e) << 16);
     }
   };
 
@@ -375,60 +391,70 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(PrefillArgs a) {
   for (int dt = 0; dt < 8; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m = -INFINITY, l = 0.f;
 
+  // Pipeline: tile t is computed from LDS buffer t % 2 while the registers receive tile t + 1;
+  // those are written to the other buffer after the MFMAs, then tile t + 2 is requested.
   load_tile(0);
+  store_tile(0);
+  if (ntiles > 1) load_tile(1);
+  __syncthreads();
   for (int tile = 0; tile < ntiles; ++tile) {
-    __syncthreads();
-#pragma unroll
-    for (int rr = 0; rr < 2; ++rr) *(uint4*)&Ks[(2 * la + rr) * kKsStride + 8 * lb] = kr[rr];
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-      *(uint32_t*)&Vt[(8 * lb + e) * kVtStride + 2 * la] = (uint32_t)elem16(vr[0], e) | ((uint32_t)elem16(vr[1], e) << 16);
-    __syncthreads();
-    if (tile + 1 < ntiles) load_tile(tile + 1);
-
+    const int buf = tile & 1;
     const int key0 = tile * kKeyTile;
-    if (key0 > wave_last) continue;  // every query of this wavefront precedes the tile
-
-    f32x4 sT[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    if (key0 <= wave_last) {  // else every query of this wavefront precedes the tile
+      const uint16_t* K = Ks + buf * kKsTile;
+      const uint16_t* V = Vt + buf * kVtTile;
+      f32x4 sT[4];
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+      for (int mt = 0; mt < 4; ++mt) {
+        sT[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const bf16x8 kf = *(const bf16x8*)&Ks[(mt * 16 + j) * kKsStride + 32 * ks + 8 * grp];
-        sT[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qfrag[ks], sT[mt], 0, 0, 0);
+        for (int ks = 0; ks < 4; ++ks) {
+          const bf16x8 kf = *(const bf16x8*)&K[(mt * 16 + j) * kKsStride + 32 * ks + 8 * grp];
+          sT[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qfrag[ks], sT[mt], 0, 0, 0);
+        }
       }
-    float s[8];
+      float s16[16];
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+      for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int key = key0 + mt * 16 + 4 * grp + rr;
-        s[mt * 4 + rr] = key <= qpos ? sT[mt][rr] * a.scale_log2 : -INFINITY;
+        for (int rr = 0; rr < 4; ++rr) {
+          const int key = key0 + mt * 16 + 4 * grp + rr;
+          s16[mt * 4 + rr] = key <= qpos ? sT[mt][rr] * a.scale_log2 : -INFINITY;
+        }
+      float bm = s16[0];
+#pragma unroll
+      for (int e = 1; e < 16; ++e) bm = fmaxf(bm, s16[e]);
+      bm = xrow_max(bm);
+      const float mn = fmaxf(m, bm);  // finite: key 0 is visible to every query
+      const float alpha = exp2f(m - mn);
+      m = mn;
+      l *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {  // keys 32h .. 32h + 31: this lane's 8 are (2h + t) * 16 + 4grp + rr
+        bf16x8 pb;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float p = exp2f(s16[8 * h + e] - mn);
+          l += p;
+          pb[e] = (__bf16)p;
+        }
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+          const uint16_t* vrow = V + (dt * 16 + j) * kVtStride + 32 * h + 4 * grp;
+          const uint2 v0 = *(const uint2*)vrow;
+          const uint2 v1 = *(const uint2*)(vrow + 16);
+          const bf16x8 va = __builtin_bit_cast(bf16x8, uint4{v0.x, v0.y, v1.x, v1.y});
+          acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb, acc[dt], 0, 0, 0);
+        }
       }
-    float bm = s[0];
-#pragma unroll
-    for (int e = 1; e < 8; ++e) bm = fmaxf(bm, s[e]);
-    bm = xrow_max(bm);
-    const float mn = fmaxf(m, bm);  // finite: key 0 is visible to every query
-    const float alpha = exp2f(m - mn);
-    m = mn;
-    l *= alpha;
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
-    bf16x8 pb;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float p = exp2f(s[e] - mn);
-      l += p;
-      pb[e] = (__bf16)p;
     }
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const uint2 v0 = *(const uint2*)&Vt[(dt * 16 + j) * kVtStride + 4 * grp];
-      const uint2 v1 = *(const uint2*)&Vt[(dt * 16 + j) * kVtStride + 16 + 4 * grp];
-      const bf16x8 va = __builtin_bit_cast(bf16x8, uint4{v0.x, v0.y, v1.x, v1.y});
-      acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb, acc[dt], 0, 0, 0);
+    if (tile + 1 < ntiles) {
+      store_tile(buf ^ 1);  // buffer of tile t - 1: every wavefront passed the barrier after it
+      if (tile + 2 < ntiles) load_tile(tile + 2);
     }
+    __syncthreads();
   }
   l = xrow_sum(l);
   if (!qvalid) return;
@@ -439,6 +465,20 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(PrefillArgs a) {
     const int d = dt * 16 + 4 * grp;
     *(uint2*)(orow + d) = uint2{pack_bf16x2(acc[dt][0] * inv, acc[dt][1] * inv), pack_bf16x2(acc[dt][2] * inv, acc[dt][3] * inv)};
   }
+}
+
+// The two K / V^T buffers exceed the 64 KB static LDS limit: dynamic LDS, attribute set once.
+template <int G>
+static int launch_prefill(const PrefillArgs& a, dim3 grid, hipStream_t s) {
+  static bool attr_set = false;
+  if (!attr_set) {
+    const hipError_t e = hipFuncSetAttribute((const void*)paged_prefill_kernel<G>,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPrefillLds);
+    if (e != hipSuccess) return fail(MSA_ERR_LAUNCH, std::string("hipFuncSetAttribute: ") + hipGetErrorString(e));
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(paged_prefill_kernel<G>, grid, dim3(256), kPrefillLds, s, a);
+  return MSA_OK;
 }
 
 }  // namespace msa
@@ -530,11 +570,13 @@ extern "C" int msa_paged_attention_prefill(const uint16_t* q, int64_t ldq, const
   a.seq_info = seq_info; a.work = work; a.scale_log2 = scale * kLog2e; a.out = out; a.ldo = ldo;
   const dim3 grid(num_work, kv_heads);
   hipStream_t s = (hipStream_t)stream;
+  int rc;
   switch (heads / kv_heads) {
-    case 1: hipLaunchKernelGGL(paged_prefill_kernel<1>, grid, dim3(256), 0, s, a); break;
-    case 2: hipLaunchKernelGGL(paged_prefill_kernel<2>, grid, dim3(256), 0, s, a); break;
-    case 4: hipLaunchKernelGGL(paged_prefill_kernel<4>, grid, dim3(256), 0, s, a); break;
+    case 1: rc = launch_prefill<1>(a, grid, s); break;
+    case 2: rc = launch_prefill<2>(a, grid, s); break;
+    case 4: rc = launch_prefill<4>(a, grid, s); break;
     default: return fail(MSA_ERR_UNSUPPORTED, "msa_paged_attention_prefill: heads / kv_heads must be 1, 2 or 4");
   }
+  if (rc != MSA_OK) return rc;
   return check_launch("msa_paged_attention_prefill");
 }
