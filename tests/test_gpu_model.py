@@ -201,6 +201,59 @@ def test_qwen3_0_6b_decode_step_batch64():
     assert all(abs(r[4]) <= 0.1 for r in report), report
 
 
+@pytest.mark.parametrize("seed", [21, 22])
+def test_qwen3_0_6b_greedy_ids_over_steps(seed):
+    """Three consecutive decode steps of the full Qwen3-0.6B-shaped int8 model at batch 64 through
+    the captured HIP graph (the measured path), step by step beside the CPU oracle (the
+    reference's bf16 op sequence) and a float64 evaluation of the same int8 model, all three fed
+    the oracle's ids.
+
+    End to end, 28 random-init bf16 layers drift apart by a few percent whichever two bf16 paths
+    are compared, so each step asserts what the single-layer tests cannot: the HIP logits are no
+    further from the float64 logits than 1.5x the oracle's own distance, the HIP path picks the
+    float64 argmax at least as often as the oracle less 2 rows, and it disagrees with the oracle
+    only where the float64 logits of the two picks are within 0.1 (each mismatch is printed)."""
+    cfg = workloads.QWEN3_0_6B
+    batch = workloads.decode_batch(64, 256, 384, seed=seed, vocab=cfg["vocab_size"], spare_blocks=64)
+    runner, ocfg, ow, okv, tables = _pair(cfg, seed=seed, max_positions=4096, num_blocks=batch.num_blocks, jitter=0.0)
+    runner.use_graphs = True
+    runner.max_model_len = 4096
+    workloads.fill_kv_pool_(runner.kv_cache, seed=seed + 1)
+    for i, (kc, vc) in enumerate(runner.kv_caches):
+        okv[i][0].copy_(kc.cpu())
+        okv[i][1].copy_(vc.cpu())
+    w64 = _dequantized64(ow)
+    kv64 = [(kc.double(), vc.double()) for kc, vc in okv]
+    tables64 = (tables[0].double(), tables[1].double())
+    rng = random.Random(seed + 2)
+    used = {b for t in batch.block_tables for b in t}
+    spare = iter(sorted(set(range(batch.num_blocks)) - used))
+    sched = []
+    for c, table, tok in zip(batch.context_lens, batch.block_tables, batch.token_ids, strict=True):
+        table = list(table)
+        if c + 3 > 16 * len(table):  # room for the next steps' tokens
+            table.append(next(spare))
+        sched.append(ScheduledChunk([rng.randrange(cfg["vocab_size"]) for _ in range(c - 1)] + [tok], c - 1, 1, table))
+    for step in range(3):
+        got = runner.forward_logits(runner.prepare(sched)).cpu()
+        graph_ids = torch.tensor([r[0] for r in runner.execute(sched)])
+        ref, ref_ids = _oracle_step(ocfg, ow, okv, tables, sched)
+        logits64, ids64 = _oracle_step(ocfg, w64, kv64, tables64, sched)
+        e_hip, e_ref = rel_l2(got, logits64), rel_l2(ref, logits64)
+        hip_exact, oracle_exact = int((graph_ids == ids64).sum()), int((ref_ids == ids64).sum())
+        bad = (graph_ids != ref_ids).nonzero().flatten().tolist()
+        report = [(i, int(graph_ids[i]), int(ref_ids[i]), float(logits64[i, ref_ids[i]] - logits64[i, graph_ids[i]]))
+                  for i in bad]
+        print(f"step {step}: rel-L2 hip-vs-float64 {e_hip:.3e}, oracle-vs-float64 {e_ref:.3e}, hip-vs-oracle "
+              f"{rel_l2(got, ref):.3e}; graph ids == oracle {64 - len(bad)}/64, == float64 {hip_exact}/64 "
+              f"(oracle {oracle_exact}/64); mismatches (row, hip, oracle, float64 gap): {report}")
+        assert e_hip <= 1.5 * e_ref, step
+        assert hip_exact >= oracle_exact - 2, step
+        assert all(abs(r[3]) <= 0.1 for r in report), report
+        sched = [ScheduledChunk(s.token_ids + [int(ref_ids[i])], len(s.token_ids), 1, s.block_table)
+                 for i, s in enumerate(sched)]
+
+
 @pytest.mark.parametrize("batch", [5, 64])
 def test_captured_decode_matches_eager(batch):
     """The HIP-graph decode step returns the eager step's ids on every replay, with eager work
