@@ -547,10 +547,25 @@ def kernel_only(mode: str, seed: int) -> int:
             else:
                 def run(i):
                     kernels.int8_linear_rows(x, ws[i], sc[i], out=y)
-            secs = hip_time(run, copies)
+            if epi == -1:
+                def run_dec(i):
+                    kernels.int8_linear_dec(x, ws[i], sc[i], norm_w=nw, eps=1e-6, out=y)
+            elif epi == kernels.EPI_SILU_MUL:
+                def run_dec(i):
+                    kernels.int8_linear_dec(x, ws[i], sc[i], epi, norm_w=nw, eps=1e-6, out=y)
+            elif epi == kernels.EPI_RESIDUAL:
+                def run_dec(i):
+                    kernels.int8_linear_dec(x, ws[i], sc[i], epi, residual=resid, out=y)
+            else:
+                def run_dec(i):
+                    kernels.int8_linear_dec(x, ws[i], sc[i], out=y)
             nbytes = linear_bytes(m, n, k)
-            print(json.dumps({"linear": name, "us_per_launch": round(secs * 1e6, 3), "bytes_per_launch": nbytes,
-                              "GB_s": round(nbytes / secs / 1e9, 1), "copies": copies}), flush=True)
+            for kind, fn in (("token-split rows kernel", run), ("decode kernel", run_dec)):
+                secs = hip_time(fn, copies)
+                label = name if not (epi == -1 and kind == "decode kernel") else "qkv [4096x1024] + input norm, 64 tokens"
+                print(json.dumps({"linear": label, "kernel": kind, "us_per_launch": round(secs * 1e6, 3),
+                                  "bytes_per_launch": nbytes, "GB_s": round(nbytes / secs / 1e9, 1),
+                                  "copies": copies}), flush=True)
             del ws, sc
         return 0
     cfg = workloads.QWEN3_0_6B

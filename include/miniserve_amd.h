@@ -95,6 +95,21 @@ int msa_int8_linear_rows(const uint16_t* x, int64_t ldx, int64_t m, int64_t k, c
                          const int8_t* qweight, const uint16_t* scale, int64_t n, int epilogue, uint16_t* y,
                          int64_t ldy, const uint16_t* residual, int64_t ldr, msa_stream_t stream);
 
+/* Int8Linear.forward (quant/int8.py:35-37) for decode-sized batches with the neighbouring ops of
+ * the layer fused: activations read straight into MFMA operand registers, each workgroup owning
+ * up to 32 tokens x 16-64 weight rows over the whole of K (no float32 partials). Activation rows
+ * are x[gather_rows[t]] (indices clamped into [0, x_rows); the embedding lookup of
+ * model/qwen3.py:148, then also copied to x_copy: the residual stream) when gather_rows is
+ * non-NULL, else x[t]. norm_w non-NULL applies RMSNorm(x) first (model/layers.py:18-22 with eps;
+ * the input_layernorm / post_attention_layernorm of model/qwen3.py:121-122). Epilogues as
+ * msa_int8_linear (MSA_EPI_RESIDUAL may write y in place over residual); gather_rows takes
+ * MSA_EPI_NONE and needs norm_w. k in {1024, 2048, 3072, 4096}; x, qweight, norm_w, x_copy
+ * 16-byte aligned with row strides % 8 == 0. */
+int msa_int8_linear_dec(const uint16_t* x, int64_t ldx, int64_t x_rows, const int64_t* gather_rows,
+                        uint16_t* x_copy, int64_t ld_copy, int64_t m, int64_t k, const uint16_t* norm_w,
+                        float eps, const int8_t* qweight, const uint16_t* scale, int64_t n, int epilogue,
+                        uint16_t* y, int64_t ldy, const uint16_t* residual, int64_t ldr, msa_stream_t stream);
+
 /* The front half of Qwen3Attention.forward (model/qwen3.py:94-98) plus the cache write of
  * paged_attention (attention/backends.py:159-160), fused with the layer's input RMSNorm
  * (model/qwen3.py:121) and, for the first layer, the embedding lookup (model/qwen3.py:148):

@@ -16,7 +16,7 @@ from pathlib import Path
 import torch  # noqa: F401  -- must be imported before the HIP library is loaded
 
 LIB_PATH = Path(__file__).resolve().parent / "libminiserve_amd.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 # name -> (restype, argtypes); mirrors include/miniserve_amd.h.
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
@@ -60,6 +60,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         c_int,
         [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_float, c_void_p, c_void_p, c_int64, c_int, c_void_p,
          c_int64, c_void_p, c_int64, c_void_p],
+    ),
+    "msa_int8_linear_dec": (
+        c_int,
+        [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_void_p, c_float, c_void_p,
+         c_void_p, c_int64, c_int, c_void_p, c_int64, c_void_p, c_int64, c_void_p],
     ),
     "msa_qkv_rope_cache_rows": (
         c_int,

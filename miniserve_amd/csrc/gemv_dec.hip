@@ -1,0 +1,463 @@
+// Decode-shaped int8 linears (a few dozen tokens per call), activations read straight into MFMA
+// operand registers.
+//
+// A workgroup of KW wavefronts owns NT 16-row weight tiles x MT 16-token tiles; wavefront ks owns
+// the ks-th of KW equal K slices (CH 64-wide chunks each), so every activation and every weight
+// byte the workgroup needs is loaded exactly once, by exactly one lane, and no LDS staging or
+// barrier stands between the loads and the MFMAs:
+//
+//  1. Every lane issues all its loads up front, unconditionally (indices are clamped instead of
+//     branched on, so the compiler's in-order load counter stays exact): its activation fragments
+//     (the A operand of v_mfma_f32_16x16x32_bf16: token row j, 16 consecutive K values per chunk),
+//     the norm weights, its int8 weight fragments (B operand: weight row j, 16 bytes per chunk),
+//     the row scales and the residual values its epilogue will add.
+//  2. RMSNorm prologue (model/layers.py:18-22 rounding: bf16(w * bf16(x * rsqrt(mean(x^2) + eps)))):
+//     each wavefront sums the squares of its K slice on bf16 pairs (v_dot2_f32_bf16), the KW
+//     partial sums of each token meet in LDS (one barrier), and each lane normalizes its own
+//     fragments in registers.
+//  3. Each 16-byte weight fragment is dequantized once to bf16(q * s) -- the value the reference's
+//     whole-matrix dequantization produces (quant/int8.py:36) -- and feeds the MT token tiles.
+//  4. The KW partial accumulators meet in LDS (second barrier); the output tiles are spread over
+//     the wavefronts, each summing the KW partials in a fixed order (deterministic) and applying
+//     the epilogue: plain bf16 store, residual add (model/qwen3.py:121-122) or silu(gate) * up with
+//     the gate and up tiles in the same workgroup (model/layers.py:77-78).
+//
+// The K mapping inside a 64-wide chunk is permuted identically for A and B (lane group g takes K
+// offsets [16g, 16g + 16) and splits them over the two MFMA k-steps), which leaves the dot
+// products unchanged and keeps each lane's weight bytes one contiguous 16-byte load.
+//
+// Block -> (row block, token chunk) is XCD-aware: the token chunks of one row block land on one
+// XCD (workgroups are dispatched round-robin over the 8 XCDs), so its weight rows come from HBM
+// once and the other chunks hit that XCD's L2.
+#include <hip/hip_runtime.h>
+
+#include "common.h"
+
+namespace msa {
+
+enum { DL_PRO_NONE = 0, DL_PRO_RMSNORM = 1, DL_PRO_GATHER_RMSNORM = 2 };
+enum { DL_EPI_NONE = 0, DL_EPI_SILU_MUL = 1, DL_EPI_RESIDUAL = 2 };
+
+struct DecLinArgs {
+  const uint16_t* x;
+  int64_t ldx;
+  int64_t x_rows;         // rows of x (gathered indices are clamped into range)
+  const int64_t* gather;  // DL_PRO_GATHER_RMSNORM: activation row of each token
+  const uint16_t* norm_w;
+  float eps;
+  uint16_t* x_copy;  // gathered rows (before the norm) are also written here when non-null
+  int64_t ld_copy;
+  int t;  // tokens
+  int k;  // in features = KW * CH * 64
+  const int8_t* w;
+  const uint16_t* scale;
+  int n;     // weight rows ([gate | up] for SILU_MUL)
+  int n_rb;  // row blocks
+  int n_tc;  // token chunks
+  uint16_t* y;
+  int64_t ldy;
+  const uint16_t* resid;
+  int64_t ldr;
+};
+
+__device__ __forceinline__ bf16x8 dequant8(uint32_t lo, uint32_t hi, float s) {
+  bf16x8 r;
+  r[0] = (__bf16)((float)(signed char)(lo) * s);
+  r[1] = (__bf16)((float)(signed char)(lo >> 8) * s);
+  r[2] = (__bf16)((float)(signed char)(lo >> 16) * s);
+  r[3] = (__bf16)((float)(signed char)(lo >> 24) * s);
+  r[4] = (__bf16)((float)(signed char)(hi) * s);
+  r[5] = (__bf16)((float)(signed char)(hi >> 8) * s);
+  r[6] = (__bf16)((float)(signed char)(hi >> 16) * s);
+  r[7] = (__bf16)((float)(signed char)(hi >> 24) * s);
+  return r;
+}
+
+// bf16(w * bf16(x * r)) on a pair of bf16 (model/layers.py:20-22).
+__device__ __forceinline__ uint32_t norm_pair(uint32_t xv, uint32_t wv, float r) {
+  const float lo = round_bf16(bf16lo(xv) * r), hi = round_bf16(bf16hi(xv) * r);
+  return pack_bf16x2(bf16lo(wv) * lo, bf16hi(wv) * hi);
+}
+
+// Weight row of tile nt, lane row j. SILU_MUL: tiles [0, NT/2) are gate rows, [NT/2, NT) the
+// matching up rows (second half of the fused [gate | up] weight, model/loader.py:41-48).
+template <int NT, int EPI>
+__device__ __forceinline__ int dec_row(const DecLinArgs& a, int rb, int nt, int j) {
+  if constexpr (EPI == DL_EPI_SILU_MUL) {
+    constexpr int NP = NT / 2;
+    return (nt < NP ? 0 : a.n / 2) + (rb * NP + nt % NP) * 16 + j;
+  } else {
+    return (rb * NT + nt) * 16 + j;
+  }
+}
+
+template <int NT, int MT, int KW, int CH, int PRO, int EPI>
+__global__ __launch_bounds__(64 * KW) __attribute__((amdgpu_waves_per_eu(1, 1))) void dec_linear_kernel(DecLinArgs a) {
+  constexpr bool NORM = PRO != DL_PRO_NONE;
+  constexpr bool GATHER = PRO == DL_PRO_GATHER_RMSNORM;
+  constexpr bool SILU = EPI == DL_EPI_SILU_MUL;
+  constexpr int NP = SILU ? NT / 2 : NT;      // output column tiles
+  constexpr int UNITS = MT * NP;              // (token tile, column tile) outputs of the workgroup
+  constexpr int UPW = (UNITS + KW - 1) / KW;  // epilogue units per wavefront
+  static_assert(!SILU || NT % 2 == 0, "SILU_MUL pairs gate and up tiles");
+  __shared__ float s_ss[KW][MT * 16];
+  // Dynamic LDS: wavefront w's activation rows [MT * 16][CH * 64 + 8] bf16, later reused for its
+  // partial accumulators [MT][NT][64] (f32x4) once its own MFMAs are done.
+  extern __shared__ f32x4 s_red[];
+
+  const int lane = threadIdx.x & 63, ks = threadIdx.x >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  const int b = blockIdx.x, xcd = b & 7, slot = b >> 3;
+  const int rb = (slot / a.n_tc) * 8 + xcd, tc = slot % a.n_tc;
+  if (rb >= a.n_rb) return;  // surplus workgroup of the XCD-rounded grid (before any barrier)
+  const int tbase = tc * MT * 16;
+  const int koff = ks * CH * 64 + g * 16;  // this lane's first K element
+
+  // ---- 1. all loads, unconditional ----
+  // Activations: this wavefront's K slice of the MT * 16 token rows (CH * 64 elements per row),
+  // read with contiguous 16-byte loads -- 32 lanes per row, two rows per instruction -- and
+  // turned into MFMA fragments through the wavefront's own LDS region below. (Fragment-shaped
+  // global loads, one token row per lane, cost several times more per byte in the vector memory
+  // pipeline.)
+  constexpr int XR = MT * 16;          // token rows
+  constexpr int XLPR = CH * 64 / 8;    // 16-byte pieces per row slice
+  constexpr int XLD = XR * XLPR / 64;  // loads per lane
+  static_assert(XLPR == 32, "two rows per load instruction");
+  const int xsub = lane >> 5, xcol = (lane & 31) * 8;
+  int64_t gidx = 0;
+  if constexpr (GATHER) {
+    const int tl = min(tbase + (lane & 31), a.t - 1);
+    const int64_t r = a.gather[tl];
+    gidx = r < 0 ? 0 : (r >= a.x_rows ? a.x_rows - 1 : r);  // memory safety only
+  }
+  const int8_t* wp[NT];
+  uint32_t scb[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int row = min(dec_row<NT, EPI>(a, rb, nt, j), a.n - 1);  // rows past n: outputs dropped
+    wp[nt] = a.w + (int64_t)row * a.k + koff;
+  }
+  // The residual values of this lane's epilogue outputs: needed last, started first.
+  uint32_t rres[UPW][4];
+  if constexpr (EPI == DL_EPI_RESIDUAL) {
+#pragma unroll
+    for (int uu = 0; uu < UPW; ++uu) {
+      const int u = min(ks + uu * KW, UNITS - 1);
+      const int mt = u / NP, nt = u % NP;
+      const int row = min(dec_row<NT, EPI>(a, rb, nt, j), a.n - 1);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int tl = min(tbase + mt * 16 + 4 * g + i, a.t - 1);
+        rres[uu][i] = a.resid[(int64_t)tl * a.ldr + row];
+      }
+    }
+  }
+  // The weights before the activations: issued after them, the compiler's scheduler sinks the
+  // weight loads below the activations' LDS writes (shorter register live ranges) and serializes
+  // the two round trips; issued first, both are in flight together.
+  uint4 wv[NT][CH];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+    for (int c = 0; c < CH; ++c) wv[nt][c] = *(const uint4*)(wp[nt] + c * 64);
+  uint4 xr[XLD];
+#pragma unroll
+  for (int i = 0; i < XLD; ++i) {
+    const int r = 2 * i + xsub;  // token row within the workgroup's tiles
+    int64_t src_row;
+    if constexpr (GATHER) {
+      src_row = __shfl(gidx, r);
+    } else {
+      src_row = min(tbase + r, a.t - 1);
+    }
+    xr[i] = *(const uint4*)(a.x + src_row * a.ldx + ks * CH * 64 + xcol);
+  }
+  uint4 nw[NORM ? CH : 1][2];
+  if constexpr (NORM) {
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      nw[c][0] = *(const uint4*)(a.norm_w + koff + c * 64);
+      nw[c][1] = *(const uint4*)(a.norm_w + koff + c * 64 + 8);
+    }
+  }
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) scb[nt] = a.scale[min(dec_row<NT, EPI>(a, rb, nt, j), a.n - 1)];
+
+  // ---- activations to MFMA fragments through this wavefront's LDS region ----
+  // Row pitch CH * 64 + 8 elements (16 bytes of padding). Each wavefront writes and then reads only
+  // its own region; the LDS operations of one wavefront complete in order, so no barrier is needed.
+  constexpr int XP = CH * 64 + 8;
+  uint16_t* xs = (uint16_t*)s_red + ks * (XR * XP);
+#pragma unroll
+  for (int i = 0; i < XLD; ++i) *(uint4*)(xs + (2 * i + xsub) * XP + xcol) = xr[i];
+  if constexpr (GATHER) {
+    // The gathered rows are the residual stream's first value (model/qwen3.py:148): one
+    // workgroup per token chunk copies them out, before the norm.
+    if (a.x_copy != nullptr && rb == 0) {
+#pragma unroll
+      for (int i = 0; i < XLD; ++i) {
+        const int tl = tbase + 2 * i + xsub;
+        if (tl < a.t) *(uint4*)(a.x_copy + (int64_t)tl * a.ld_copy + ks * CH * 64 + xcol) = xr[i];
+      }
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  uint4 xa[MT][CH][2];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) xa[mt][c][h] = *(const uint4*)(xs + (mt * 16 + j) * XP + g * 16 + c * 64 + h * 8);
+
+  // ---- 2. RMSNorm prologue ----
+  if constexpr (NORM) {
+    float ss[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      float s = 0.f;
+#pragma unroll
+      for (int c = 0; c < CH; ++c)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          s = dot2_bf16(xa[mt][c][h].x, xa[mt][c][h].x, s);
+          s = dot2_bf16(xa[mt][c][h].y, xa[mt][c][h].y, s);
+          s = dot2_bf16(xa[mt][c][h].z, xa[mt][c][h].z, s);
+          s = dot2_bf16(xa[mt][c][h].w, xa[mt][c][h].w, s);
+        }
+      s += __shfl_xor(s, 16);
+      s += __shfl_xor(s, 32);
+      ss[mt] = s;
+    }
+    if (g == 0) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) s_ss[ks][mt * 16 + j] = ss[mt];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      float tot = 0.f;
+#pragma unroll
+      for (int w = 0; w < KW; ++w) tot += s_ss[w][mt * 16 + j];
+      const float r = 1.0f / sqrtf(tot / (float)a.k + a.eps);
+#pragma unroll
+      for (int c = 0; c < CH; ++c)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          uint4& v = xa[mt][c][h];
+          const uint4 wn = nw[c][h];
+          v = uint4{norm_pair(v.x, wn.x, r), norm_pair(v.y, wn.y, r), norm_pair(v.z, wn.z, r),
+                    norm_pair(v.w, wn.w, r)};
+        }
+    }
+  }
+
+  // ---- 3. dequantize once, MFMA over the MT token tiles ----
+  float sc[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) sc[nt] = bf16_to_f32(scb[nt]);
+  f32x4 acc[MT][NT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < CH; ++c)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const bf16x8 bv = h == 0 ? dequant8(wv[nt][c].x, wv[nt][c].y, sc[nt]) : dequant8(wv[nt][c].z, wv[nt][c].w, sc[nt]);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xa[mt][c][h]), bv,
+                                                                acc[mt][nt], 0, 0, 0);
+      }
+
+  // ---- 4. K slices meet in LDS; epilogue spread over the wavefronts ----
+  constexpr int XSLOT = XR * XP * 2 / 16;  // f32x4 per wavefront region
+  static_assert(MT * NT * 64 <= XSLOT, "partials fit the wavefront's activation region");
+  if constexpr (KW > 1) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) s_red[ks * XSLOT + (mt * NT + nt) * 64 + lane] = acc[mt][nt];
+    __syncthreads();
+  }
+#pragma unroll
+  for (int uu = 0; uu < UPW; ++uu) {
+    const int u = ks + uu * KW;
+    if (u >= UNITS) break;
+    const int mt = u / NP, np = u % NP;
+    f32x4 v0 = f32x4{0.f, 0.f, 0.f, 0.f}, v1 = f32x4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (KW > 1) {
+#pragma unroll
+      for (int w = 0; w < KW; ++w) {
+        v0 += s_red[w * XSLOT + (mt * NT + np) * 64 + lane];
+        if constexpr (SILU) v1 += s_red[w * XSLOT + (mt * NT + np + NP) * 64 + lane];
+      }
+    } else {
+      v0 = acc[mt][np];
+      if constexpr (SILU) v1 = acc[mt][np + NP];
+    }
+    const int col = SILU ? (rb * NP + np) * 16 + j : dec_row<NT, EPI>(a, rb, np, j);
+    const int ncols = SILU ? a.n / 2 : a.n;
+    if (col >= ncols) continue;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int tl = tbase + mt * 16 + 4 * g + i;
+      if (tl >= a.t) continue;
+      float o;
+      if constexpr (SILU) {
+        const float gt = round_bf16(v0[i]), up = round_bf16(v1[i]);
+        o = round_bf16(gt / (1.0f + expf(-gt))) * up;
+      } else if constexpr (EPI == DL_EPI_RESIDUAL) {
+        o = round_bf16(v0[i]) + bf16_to_f32(rres[uu][i]);
+      } else {
+        o = v0[i];
+      }
+      a.y[(int64_t)tl * a.ldy + col] = f32_to_bf16(o);
+    }
+  }
+}
+
+// ---- host side ----------------------------------------------------------------------------------
+
+struct DecShape {
+  int kw;  // wavefronts per workgroup (K slices)
+  int nt;  // 16-row weight tiles per workgroup
+  int mt;  // 16-token tiles per workgroup
+};
+
+constexpr int kDecCh = 4;  // 64-wide K chunks per wavefront
+
+// The K split: k = 64 * 4 * KW for KW in {4, 8, 12, 16} (k = 1024, 2048, 3072, 4096).
+static int dec_kw(int64_t k) {
+  if (k % 256 != 0) return 0;
+  const int64_t kw = k / 256;
+  return (kw == 4 || kw == 8 || kw == 12 || kw == 16) ? (int)kw : 0;
+}
+
+static DecShape dec_shape(int64_t m, int64_t k, int epi) {
+  DecShape s{dec_kw(k), 1, 1};
+  if (epi == DL_EPI_SILU_MUL) {
+    s.nt = s.kw <= 8 ? 4 : 2;
+    s.mt = (m > 16 && s.kw <= 8) ? 2 : 1;
+  } else if (epi == DL_EPI_NONE) {
+    s.nt = m > 16 ? 2 : 1;
+    s.mt = (m > 16 && s.kw <= 8) ? 2 : 1;
+  }
+  return s;
+}
+
+template <int NT, int MT, int KW, int PRO, int EPI>
+static int dec_launch(const DecLinArgs& a, hipStream_t s) {
+  const size_t lds = (size_t)KW * MT * 16 * (kDecCh * 64 + 8) * 2;
+  const int blocks = ((a.n_rb + 7) / 8) * 8 * a.n_tc;
+  auto kernel = dec_linear_kernel<NT, MT, KW, kDecCh, PRO, EPI>;
+  if (lds > 64 * 1024) {
+    hipError_t e = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return fail(MSA_ERR_LAUNCH, std::string("hipFuncSetAttribute: ") + hipGetErrorString(e));
+  }
+  hipLaunchKernelGGL(kernel, dim3(blocks), dim3(64 * KW), lds, s, a);
+  return MSA_OK;
+}
+
+template <int NT, int MT, int PRO, int EPI>
+static int dec_dispatch_kw(int kw, const DecLinArgs& a, hipStream_t s) {
+  switch (kw) {
+    case 4: return dec_launch<NT, MT, 4, PRO, EPI>(a, s);
+    case 8: return dec_launch<NT, MT, 8, PRO, EPI>(a, s);
+    case 12: return dec_launch<NT, MT, 12, PRO, EPI>(a, s);
+    case 16: return dec_launch<NT, MT, 16, PRO, EPI>(a, s);
+    default: return fail(MSA_ERR_UNSUPPORTED, "decode linear: unsupported in_features");
+  }
+}
+
+template <int PRO, int EPI>
+static int dec_dispatch(const DecShape& sh, const DecLinArgs& a, hipStream_t s) {
+  if constexpr (EPI == DL_EPI_SILU_MUL) {
+    if (sh.nt == 4 && sh.mt == 2) return dec_dispatch_kw<4, 2, PRO, EPI>(sh.kw, a, s);
+    if (sh.nt == 4 && sh.mt == 1) return dec_dispatch_kw<4, 1, PRO, EPI>(sh.kw, a, s);
+    return dec_dispatch_kw<2, 1, PRO, EPI>(sh.kw, a, s);
+  } else if constexpr (EPI == DL_EPI_NONE) {
+    if (sh.mt == 2) return dec_dispatch_kw<2, 2, PRO, EPI>(sh.kw, a, s);
+    if (sh.nt == 2) return dec_dispatch_kw<2, 1, PRO, EPI>(sh.kw, a, s);
+    return dec_dispatch_kw<1, 1, PRO, EPI>(sh.kw, a, s);
+  } else {
+    return dec_dispatch_kw<1, 1, PRO, EPI>(sh.kw, a, s);
+  }
+}
+
+bool dec_linear_supported(int64_t k) { return dec_kw(k) != 0; }
+
+int launch_dec_linear(const uint16_t* x, int64_t ldx, int64_t x_rows, const int64_t* gather, uint16_t* x_copy,
+                      int64_t ld_copy, int64_t m, int64_t k, const uint16_t* norm_w, float eps, const int8_t* qweight,
+                      const uint16_t* scale, int64_t n, int epilogue, uint16_t* y, int64_t ldy,
+                      const uint16_t* residual, int64_t ldr, hipStream_t s) {
+  const DecShape sh = dec_shape(m, k, epilogue);
+  if (sh.kw == 0) return fail(MSA_ERR_UNSUPPORTED, "decode linear: in_features must be 1024, 2048, 3072 or 4096");
+  const int np = epilogue == DL_EPI_SILU_MUL ? sh.nt / 2 : sh.nt;
+  const int64_t cols = epilogue == DL_EPI_SILU_MUL ? n / 2 : n;
+  DecLinArgs a{};
+  a.x = x; a.ldx = ldx; a.x_rows = x_rows; a.gather = gather; a.norm_w = norm_w; a.eps = eps;
+  a.x_copy = x_copy; a.ld_copy = ld_copy; a.t = (int)m; a.k = (int)k; a.w = qweight; a.scale = scale; a.n = (int)n;
+  a.n_rb = (int)((cols + 16 * np - 1) / (16 * np));
+  a.n_tc = (int)((m + 16 * sh.mt - 1) / (16 * sh.mt));
+  a.y = y; a.ldy = ldy; a.resid = residual; a.ldr = ldr;
+  int rc;
+  const int pro = gather ? DL_PRO_GATHER_RMSNORM : (norm_w ? DL_PRO_RMSNORM : DL_PRO_NONE);
+  if (pro == DL_PRO_GATHER_RMSNORM) {
+    if (epilogue != DL_EPI_NONE) return fail(MSA_ERR_UNSUPPORTED, "decode linear: gathered rows take MSA_EPI_NONE");
+    rc = dec_dispatch<DL_PRO_GATHER_RMSNORM, DL_EPI_NONE>(sh, a, s);
+  } else if (epilogue == DL_EPI_SILU_MUL) {
+    rc = pro == DL_PRO_RMSNORM ? dec_dispatch<DL_PRO_RMSNORM, DL_EPI_SILU_MUL>(sh, a, s)
+                               : dec_dispatch<DL_PRO_NONE, DL_EPI_SILU_MUL>(sh, a, s);
+  } else if (epilogue == DL_EPI_NONE) {
+    rc = pro == DL_PRO_RMSNORM ? dec_dispatch<DL_PRO_RMSNORM, DL_EPI_NONE>(sh, a, s)
+                               : dec_dispatch<DL_PRO_NONE, DL_EPI_NONE>(sh, a, s);
+  } else if (epilogue == DL_EPI_RESIDUAL) {
+    rc = pro == DL_PRO_RMSNORM ? dec_dispatch<DL_PRO_RMSNORM, DL_EPI_RESIDUAL>(sh, a, s)
+                               : dec_dispatch<DL_PRO_NONE, DL_EPI_RESIDUAL>(sh, a, s);
+  } else {
+    return fail(MSA_ERR_INVALID, "decode linear: unknown epilogue");
+  }
+  if (rc != MSA_OK) return rc;
+  return check_launch("decode linear");
+}
+
+}  // namespace msa
+
+using namespace msa;
+
+extern "C" int msa_int8_linear_dec(const uint16_t* x, int64_t ldx, int64_t x_rows, const int64_t* gather_rows,
+                                   uint16_t* x_copy, int64_t ld_copy, int64_t m, int64_t k, const uint16_t* norm_w,
+                                   float eps, const int8_t* qweight, const uint16_t* scale, int64_t n, int epilogue,
+                                   uint16_t* y, int64_t ldy, const uint16_t* residual, int64_t ldr,
+                                   msa_stream_t stream) {
+  if (m == 0) return MSA_OK;
+  if (!x || !qweight || !scale || !y) return fail(MSA_ERR_INVALID, "msa_int8_linear_dec: null pointer");
+  if (m < 0 || n <= 0 || k <= 0 || m > 0x7fffffff || n > 0x7fffffff)
+    return fail(MSA_ERR_INVALID, "msa_int8_linear_dec: bad shape");
+  if (!dec_linear_supported(k))
+    return fail(MSA_ERR_UNSUPPORTED, "msa_int8_linear_dec: in_features must be 1024, 2048, 3072 or 4096");
+  if (ldx < k || ldx % 8 != 0 || !aligned16(x) || !aligned16(qweight))
+    return fail(MSA_ERR_INVALID, "msa_int8_linear_dec: x / qweight must be 16-byte aligned with ldx % 8 == 0");
+  if (norm_w && !aligned16(norm_w)) return fail(MSA_ERR_INVALID, "msa_int8_linear_dec: norm_w must be 16-byte aligned");
+  if (gather_rows && !norm_w) return fail(MSA_ERR_UNSUPPORTED, "msa_int8_linear_dec: gather_rows needs norm_w");
+  if (gather_rows && epilogue != MSA_EPI_NONE)
+    return fail(MSA_ERR_UNSUPPORTED, "msa_int8_linear_dec: gather_rows takes MSA_EPI_NONE");
+  if (x_rows < (gather_rows ? 1 : m)) return fail(MSA_ERR_INVALID, "msa_int8_linear_dec: x has too few rows");
+  if (x_copy && (!gather_rows || !aligned16(x_copy) || ld_copy < k || ld_copy % 8 != 0))
+    return fail(MSA_ERR_INVALID, "msa_int8_linear_dec: x_copy needs gather_rows, 16-byte alignment and ld_copy >= k");
+  if (epilogue == MSA_EPI_SILU_MUL && n % 2 != 0)
+    return fail(MSA_ERR_INVALID, "msa_int8_linear_dec: SILU_MUL needs an even n");
+  const int64_t out_cols = epilogue == MSA_EPI_SILU_MUL ? n / 2 : n;
+  if (ldy < out_cols) return fail(MSA_ERR_INVALID, "msa_int8_linear_dec: ldy too small");
+  if (epilogue == MSA_EPI_RESIDUAL && (!residual || ldr < n))
+    return fail(MSA_ERR_INVALID, "msa_int8_linear_dec: the residual epilogue needs residual with ldr >= n");
+  return launch_dec_linear(x, ldx, x_rows, gather_rows, x_copy, ld_copy, m, k, norm_w, eps, qweight, scale, n,
+                           epilogue, y, ldy, residual, ldr, (hipStream_t)stream);
+}

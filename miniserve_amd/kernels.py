@@ -398,6 +398,65 @@ def int8_linear_rows(
     return out
 
 
+DEC_MAX_TOKENS = 128  # decode-sized batches the pipeline sends to msa_int8_linear_dec
+
+
+def dec_supported(k: int) -> bool:
+    """Whether msa_int8_linear_dec takes this in_features (K split over 4-16 wavefronts of four
+    64-wide chunks each)."""
+    return k in (1024, 2048, 3072, 4096)
+
+
+def int8_linear_dec(
+    x: Tensor,
+    qweight: Tensor,
+    scale: Tensor,
+    epilogue: int = EPI_NONE,
+    residual: Tensor | None = None,
+    out: Tensor | None = None,
+    norm_w: Tensor | None = None,
+    eps: float = 0.0,
+    gather: Tensor | None = None,
+    x_copy: Tensor | None = None,
+) -> Tensor:
+    """y = [RMSNorm]([x[gather]]) @ bf16(qweight * scale)^T with the epilogue fused, for
+    decode-sized batches (msa_int8_linear_dec).
+
+    x [rows, k] bf16. ``gather`` (int64 [m]) takes the activation rows x[gather] (the embedding
+    lookup) and, with ``x_copy`` [m, k], also writes them there (the residual stream); it needs
+    ``norm_w`` and EPI_NONE. ``norm_w`` applies RMSNorm (model/layers.py:18-22) before the product.
+    EPI_RESIDUAL returns residual + y and may write in place (out=residual).
+    """
+    _on_gpu(x, qweight, scale)
+    _check(x.dtype == torch.bfloat16 and x.dim() == 2 and x.stride(-1) == 1, "int8_linear_dec: x [rows, k] bf16")
+    _check(qweight.dtype == torch.int8 and qweight.is_contiguous(), "int8_linear_dec: bad qweight")
+    n, k = qweight.shape
+    _check(x.shape[1] == k, "int8_linear_dec: x / weight feature mismatch")
+    if gather is not None:
+        _check(gather.dtype == torch.int64 and gather.dim() == 1 and gather.is_contiguous(), "int8_linear_dec: gather")
+        m = gather.numel()
+    else:
+        m = x.shape[0]
+    cols = n // 2 if epilogue == EPI_SILU_MUL else n
+    if out is None:
+        out = torch.empty(m, cols, dtype=torch.bfloat16, device=x.device)
+    _check(out.shape == (m, cols) and out.stride(-1) == 1, "int8_linear_dec: bad out")
+    r2 = None
+    if epilogue == EPI_RESIDUAL:
+        _check(residual is not None and residual.shape == (m, n) and residual.stride(-1) == 1, "int8_linear_dec: residual")
+        r2 = residual
+    if norm_w is not None:
+        _check(norm_w.dtype == torch.bfloat16 and norm_w.numel() == k, "int8_linear_dec: norm weight")
+    if x_copy is not None:
+        _check(x_copy.shape == (m, k) and x_copy.stride(-1) == 1, "int8_linear_dec: x_copy")
+    _native.call(
+        "msa_int8_linear_dec", _ptr(x), x.stride(0), x.shape[0], _ptr(gather), _ptr(x_copy),
+        x_copy.stride(0) if x_copy is not None else 0, m, k, _ptr(norm_w), float(eps), _ptr(qweight), _ptr(scale), n,
+        epilogue, _ptr(out), out.stride(0), _ptr(r2), r2.stride(0) if r2 is not None else 0, _stream(x),
+    )
+    return out
+
+
 def qkv_rope_cache_rows(
     x: Tensor,
     qweight: Tensor,

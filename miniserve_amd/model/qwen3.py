@@ -226,6 +226,15 @@ class Qwen3ForCausalLM(nn.Module):
         pos = positions if positions.dtype == torch.int64 and positions.is_contiguous() else positions.long().contiguous()
         residual = torch.empty(t, cfg.hidden_size, dtype=torch.bfloat16, device=ids.device)
         rot = self.rotary
+
+        def lin(k: int):
+            # Up to DEC_MAX_TOKENS tokens the decode kernel (activations straight into MFMA
+            # operands, all loads in flight at once) serves the K it supports; else the
+            # token-split rows kernel.
+            if t <= kernels.DEC_MAX_TOKENS and kernels.dec_supported(k):
+                return kernels.int8_linear_dec
+            return kernels.int8_linear_rows
+
         for i, (layer, (k_cache, v_cache)) in enumerate(zip(self.layers, kv_caches, strict=True)):
             attn, mlp = layer.self_attn, layer.mlp
             qkv, o, gu, dn = attn.qkv_proj, attn.o_proj, mlp.gate_up_proj, mlp.down_proj
@@ -237,12 +246,12 @@ class Qwen3ForCausalLM(nn.Module):
                 eps=layer.input_layernorm.eps, gather=ids if first else None, x_copy=residual if first else None,
             )
             a = attend(q, k_cache, v_cache, meta, attn.scale).view(t, attn.q_size)
-            kernels.int8_linear_rows(a, o.qweight, o.scale, kernels.EPI_RESIDUAL, residual=residual, out=residual)
-            act = kernels.int8_linear_rows(
+            lin(attn.q_size)(a, o.qweight, o.scale, kernels.EPI_RESIDUAL, residual=residual, out=residual)
+            act = lin(cfg.hidden_size)(
                 residual, gu.qweight, gu.scale, kernels.EPI_SILU_MUL,
                 norm_w=layer.post_attention_layernorm.weight, eps=layer.post_attention_layernorm.eps,
             )
-            kernels.int8_linear_rows(act, dn.qweight, dn.scale, kernels.EPI_RESIDUAL, residual=residual, out=residual)
+            lin(cfg.intermediate_size)(act, dn.qweight, dn.scale, kernels.EPI_RESIDUAL, residual=residual, out=residual)
         return residual
 
     def _fused_forward(

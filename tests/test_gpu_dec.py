@@ -1,0 +1,141 @@
+"""GPU parity of the decode-shaped int8 linear (msa_int8_linear_dec: activations straight into MFMA
+operand registers, RMSNorm prologue, embedding gather, residual / silu * up epilogues) against the
+CPU oracle on the same seeded inputs.
+
+Bars: within rel-L2 1e-2 of the oracle and within bf16 rounding (4e-3) of a float64 product of
+the same dequantized weights; gathered rows bit-exact; the residual add exact on the kernel's own
+projection; the fused norm within 5e-3 of the norm kernel followed by the plain product; results
+bit-identical across calls. Every call goes through the C ABI.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+from helpers import rel_l2
+
+from miniserve_amd import kernels
+from oracle import int8 as oi
+from oracle import layers as ol
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+def _bf16(shape, seed, std=1.0):
+    return (torch.randn(shape, generator=torch.Generator().manual_seed(seed)) * std).to(torch.bfloat16)
+
+
+def _weights(n, k, seed):
+    return oi.quantize_int8(_bf16((n, k), seed, std=0.02))
+
+
+def _norm_w(dim, seed):
+    return (1 + 0.1 * torch.randn(dim, generator=torch.Generator().manual_seed(seed))).to(torch.bfloat16)
+
+
+DEC_SHAPES = [
+    (1, 1024, 2048),
+    (5, 4096, 1024),
+    (16, 3072, 1024),  # the gate_proj-shaped single linear
+    (17, 1000, 1024),  # ragged rows and a ragged last row block
+    (64, 4096, 1024),  # qkv
+    (64, 1024, 2048),  # o
+    (64, 1024, 3072),  # down
+    (100, 512, 4096),
+    (256, 1024, 1024),
+    (3, 48, 3072),  # fewer rows than one row block
+]
+
+
+@pytest.mark.parametrize("m,n,k", DEC_SHAPES)
+def test_dec_linear(m, n, k):
+    q, s = _weights(n, k, seed=n + k)
+    x = _bf16((m, k), seed=m)
+    qd, sd, xd = q.to(DEV), s.to(DEV), x.to(DEV)
+    y = kernels.int8_linear_dec(xd, qd, sd)
+    y2 = kernels.int8_linear_dec(xd, qd, sd)
+    assert torch.equal(y, y2)  # deterministic
+    ref = oi.int8_linear(x, q, s)
+    exact = x.double() @ oi.dequantize(q, s, torch.bfloat16).double().T
+    assert rel_l2(y.cpu(), ref) < 1e-2
+    assert rel_l2(y.cpu(), exact) < 4e-3
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 1024, 3072), (64, 1024, 2048), (64, 1024, 3072), (37, 1024, 1024),
+                                   (70, 4096, 4096)])
+def test_dec_residual_in_place(m, n, k):
+    q, s = _weights(n, k, seed=3 * n + k)
+    x = _bf16((m, k), seed=m + 1)
+    r = _bf16((m, n), seed=m + 2)
+    rd = r.to(DEV)
+    out = kernels.int8_linear_dec(x.to(DEV), q.to(DEV), s.to(DEV), kernels.EPI_RESIDUAL, residual=rd, out=rd)
+    assert out.data_ptr() == rd.data_ptr()
+    ref = r + oi.int8_linear(x, q, s)
+    assert rel_l2(rd.cpu(), ref) < 1e-2
+    y = kernels.int8_linear_dec(x.to(DEV), q.to(DEV), s.to(DEV)).cpu()
+    assert torch.equal(rd.cpu(), r + y)  # the residual add itself is exact on the kernel's projection
+
+
+@pytest.mark.parametrize("m,k", [(1, 1024), (16, 1024), (64, 1024), (77, 1024), (200, 1024), (9, 4096)])
+@pytest.mark.parametrize("with_norm", [True, False])
+def test_dec_silu_mul(m, k, with_norm):
+    n = 6144 if k == 1024 else 2048
+    q, s = _weights(n, k, seed=m + k)
+    x = _bf16((m, k), seed=m + 5)
+    w = _norm_w(k, seed=m + 6)
+    y = kernels.int8_linear_dec(
+        x.to(DEV), q.to(DEV), s.to(DEV), kernels.EPI_SILU_MUL, norm_w=w.to(DEV) if with_norm else None, eps=1e-6
+    )
+    h = ol.rms_norm(x, w, 1e-6) if with_norm else x
+    gate, up = oi.int8_linear(h, q, s).chunk(2, dim=-1)
+    ref = torch.nn.functional.silu(gate) * up
+    assert y.shape == (m, n // 2)
+    assert rel_l2(y.cpu(), ref) < 1e-2
+    if with_norm:  # against the norm kernel followed by the plain fused product
+        hd = kernels.rmsnorm(x.to(DEV), w.to(DEV), 1e-6)
+        plain = kernels.int8_linear_dec(hd, q.to(DEV), s.to(DEV), kernels.EPI_SILU_MUL)
+        assert rel_l2(y.cpu(), plain.cpu()) < 5e-3
+
+
+@pytest.mark.parametrize("m,n,k", [(64, 4096, 1024), (1, 4096, 1024), (33, 6144, 4096)])
+def test_dec_norm_prologue(m, n, k):
+    """RMSNorm + product (the qkv projection after input_layernorm)."""
+    q, s = _weights(n, k, seed=m + n)
+    x = _bf16((m, k), seed=m + 7, std=3.0)
+    w = _norm_w(k, seed=m + 8)
+    y = kernels.int8_linear_dec(x.to(DEV), q.to(DEV), s.to(DEV), norm_w=w.to(DEV), eps=1e-6).cpu()
+    h = ol.rms_norm(x, w, 1e-6)
+    assert rel_l2(y, oi.int8_linear(h, q, s)) < 1e-2
+    assert rel_l2(y, h.double() @ oi.dequantize(q, s, torch.bfloat16).double().T) < 4e-3
+    # against the norm kernel followed by the plain product (the two sum the squares in different
+    # float32 orders, so a rounding boundary may fall differently on a few elements)
+    hd = kernels.rmsnorm(x.to(DEV), w.to(DEV), 1e-6)
+    plain = kernels.int8_linear_dec(hd, q.to(DEV), s.to(DEV)).cpu()
+    assert rel_l2(y, plain) < 1e-3
+
+
+@pytest.mark.parametrize("t", [1, 64, 70])
+def test_dec_gather_embedding(t):
+    """Layer 0: rows gathered from the embedding table (copied out as the residual stream), RMSNorm,
+    product."""
+    vocab, k, n = 997, 1024, 4096
+    table = _bf16((vocab, k), seed=t, std=0.02)
+    ids = torch.randint(0, vocab, (t,), generator=torch.Generator().manual_seed(t + 1))
+    q, s = _weights(n, k, seed=t + 2)
+    w = _norm_w(k, seed=t + 3)
+    resid = torch.full((t, k), 7.0, dtype=torch.bfloat16, device=DEV)
+    y = kernels.int8_linear_dec(table.to(DEV), q.to(DEV), s.to(DEV), norm_w=w.to(DEV), eps=1e-6,
+                                gather=ids.to(DEV), x_copy=resid).cpu()
+    x = table[ids]
+    assert torch.equal(resid.cpu(), x)  # the embedding rows, bit for bit
+    h = ol.rms_norm(x, w, 1e-6)
+    assert rel_l2(y, oi.int8_linear(h, q, s)) < 1e-2
+    plain = kernels.int8_linear_dec(x.to(DEV), q.to(DEV), s.to(DEV), norm_w=w.to(DEV), eps=1e-6).cpu()
+    assert torch.equal(y, plain)
+
+
+def test_dec_rejects_unsupported_k():
+    q, s = _weights(64, 512, seed=1)
+    with pytest.raises(RuntimeError, match="in_features"):
+        kernels.int8_linear_dec(_bf16((4, 512), 2).to(DEV), q.to(DEV), s.to(DEV))
