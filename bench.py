@@ -44,7 +44,10 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0
 BATCH, CTX_LO, CTX_HI = 64, 256, 384
 # FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 of one decode-attention launch on the decode workload, from
 # rocprofv3 --pmc: 42,618.69 KiB x 2 x 1024 + 256 KiB x 1024 (profiles/paged_decode_kernel_traffic_pmc.md).
-ATTN_TRAFFIC_BYTES: int | None = 87_545_221
+# FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 of one fused decode-attention launch on the decode workload,
+# from rocprofv3 --pmc: 42,902.07 KiB x 2 x 1024 + 512 KiB x 1024
+# (profiles/paged_decode_kernel_traffic_pmc.md).
+ATTN_TRAFFIC_BYTES: int | None = 88_387_737
 
 
 def log(msg: str) -> None:
@@ -125,6 +128,17 @@ def attention_bytes(ctx: list[int], heads: int, kv_heads: int, dim: int) -> int:
     return kv + qo + tables + 8 * len(ctx)
 
 
+def attention_qkv_bytes(ctx: list[int], heads: int, kv_heads: int, dim: int) -> int:
+    """One fused decode-attention launch (per-head norms, RoPE, KV write, attention): the cached K and
+    V of every earlier context token for every KV head, each sequence's qkv projection row, its new
+    key and value written to the cache, its outputs, the rotary rows of its position (float32 cos
+    and sin), the block-table entries read and the per-sequence ints."""
+    kv = 2 * kv_heads * dim * 2 * sum(c - 1 for c in ctx)
+    rows = len(ctx) * ((heads + 2 * kv_heads) * dim * 2 + 2 * kv_heads * dim * 2 + heads * dim * 2 + 2 * dim * 4)
+    tables = 4 * sum(-(-c // 16) for c in ctx)
+    return kv + rows + tables + 16 * len(ctx)
+
+
 def linear_bytes(m: int, n: int, k: int) -> int:
     """One int8 linear: int8 weights, bf16 scales, bf16 x in, bf16 y out."""
     return n * k + 2 * n + 2 * m * k + 2 * m * n
@@ -153,28 +167,57 @@ def decode_sched(cfg: dict, batch, seed: int):
     return sched
 
 
-def time_layer_attention(runner, sched, cfg) -> tuple[float, int, str]:
-    """The dominant decode kernel: one decode-attention launch per layer (distinct KV pools) per
-    pass; returns (seconds per launch, algorithmic bytes per launch, kernel name)."""
+def time_layer_attention(runner, sched, cfg, fused: bool = True) -> tuple[float, int, str]:
+    """The dominant decode kernel as the step runs it -- ``fused``: per-head q/k-norm, RoPE, KV write
+    and attention from the qkv projection rows (the token-split decode step); else attention from
+    normed, rotated q after a separate cache write (larger batches) -- one launch per layer
+    (distinct KV pools) per pass on the step's own metadata; returns (seconds per launch,
+    algorithmic bytes per launch, kernel name)."""
     import torch
 
     from miniserve_amd import kernels
+    from miniserve_amd.model.layers import RotaryEmbedding
 
     inp = runner.prepare(sched)
     d = inp.attn.decode
+    dev = runner.device
     heads, kvh, dim = cfg["num_attention_heads"], cfg["num_key_value_heads"], cfg["head_dim"]
     ptok, parts = kernels.decode_splits(d.num_seqs, kvh, d.block_tables.shape[1])
-    q = torch.randn(len(sched), heads, dim, device=runner.device).to(torch.bfloat16)
-    out = torch.empty_like(q)
+    g = torch.Generator(device=dev).manual_seed(5)
+    out = torch.empty(len(sched), heads, dim, dtype=torch.bfloat16, device=dev)
     caches = runner.kv_caches
+    ctx = [s.num_computed + 1 for s in sched]
+    if not fused:
+        q = torch.randn(len(sched), heads, dim, device=dev, generator=g).to(torch.bfloat16)
+
+        def launch_plain(i):
+            kc, vc = caches[i]
+            kernels.paged_attention_decode(q, kc, vc, d.block_tables, d.context_lens, d.q_rows, ptok, parts,
+                                           dim**-0.5, out)
+
+        secs = hip_time(launch_plain, len(caches), reps=4)
+        return secs, attention_bytes(ctx, heads, kvh, dim), f"paged_decode_kernel<{heads // kvh}, 4, false>"
+    qkv = torch.randn(len(sched), (heads + 2 * kvh) * dim, device=dev, generator=g).to(torch.bfloat16)
+    model = getattr(runner, "model", None)
+    if model is not None:
+        cos_t, sin_t = model.rotary.cos, model.rotary.sin
+        norms = [(ly.self_attn.q_norm.weight, ly.self_attn.k_norm.weight) for ly in model.layers]
+    else:  # the kernel-only entry point has no model: the same tables, unit norm weights
+        rot = RotaryEmbedding(dim, max(ctx) + 1, cfg["rope_theta"])
+        rot.build(dev)
+        cos_t, sin_t = rot.cos, rot.sin
+        ones = torch.ones(dim, dtype=torch.bfloat16, device=dev)
+        norms = [(ones, ones)] * len(caches)
 
     def launch(i):
         kc, vc = caches[i]
-        kernels.paged_attention_decode(q, kc, vc, d.block_tables, d.context_lens, d.q_rows, ptok, parts, dim**-0.5, out)
+        qw, kw = norms[i]
+        kernels.paged_attention_decode_qkv(qkv, heads, qw, kw, cfg["rms_norm_eps"], cos_t, sin_t,
+                                           inp.attn.slot_mapping, kc, vc, d.block_tables, d.context_lens, d.q_rows,
+                                           ptok, parts, dim**-0.5, out)
 
     secs = hip_time(launch, len(caches), reps=4)
-    ctx = [s.num_computed + 1 for s in sched]
-    return secs, attention_bytes(ctx, heads, kvh, dim), f"paged_decode_kernel<{heads // kvh}, 4>"
+    return secs, attention_qkv_bytes(ctx, heads, kvh, dim), f"paged_decode_kernel<{heads // kvh}, 4, true>"
 
 
 def time_graph_steps(runner, sched, steps: int, warmup: int) -> float:
@@ -453,7 +496,7 @@ def bench_decode8b(args) -> dict:
         f"({runner.kv_cache.numel() * 2 / 1e9:.1f} GB)")
     dt = time_graph_steps(runner, sched, args.steps, args.warmup)
     log(f"graph {args.steps} steps: {dt * 1e3:.3f} ms/step, {nseq / dt:.0f} tok/s")
-    secs, nbytes, kname = time_layer_attention(runner, sched, cfg)
+    secs, nbytes, kname = time_layer_attention(runner, sched, cfg, fused=False)
     log(f"decode attention: {secs * 1e6:.2f} us/launch, {nbytes / secs / 1e9:.0f} GB/s")
     out = line("decode tok/s at batch 256 (Qwen3-8B-shaped int8, contexts U[512,4096])", nseq / dt, "tok/s", args,
                dt * 1e3, {"workload": "Qwen3-8B-architecture int8 decode step (36 layers, untied bf16 LM head, "

@@ -213,6 +213,27 @@ int msa_paged_attention_decode(const uint16_t* q, int64_t ldq, const uint16_t* k
                                int partition_tokens, int max_partitions, float scale, uint16_t* out,
                                int64_t ldo, void* workspace, size_t workspace_bytes, msa_stream_t stream);
 
+/* The decode rows of Qwen3Attention.forward from the projection onward (model/qwen3.py:95-99 with
+ * the cache write of attention/backends.py:159-160) in one launch: qkv [*, (H + 2 KVH) * 128]
+ * holds the int8 qkv projection rows [q | k | v] (row stride ldqkv, model/loader.py:22-28). For
+ * sequence i (row q_rows[i]) the new token sits at position p = context_lens[i] - 1
+ * (runner/model_runner.py:186-189): each workgroup applies the per-head RMSNorm (q_norm_w /
+ * k_norm_w, qk_eps) and RoPE at p (float32 tables [max_positions, 128], model/layers.py:43-65) to
+ * its query heads and its KV head's key, writes the key and value into k_cache / v_cache at slot
+ * slot_mapping[q_rows[i]] (int64; slots outside [0, num_slots) are not written -- the runner's
+ * slot is block_tables[i, p / 16] * 16 + p % 16), and attends to keys 0..p-1 from the cache and to
+ * key p from registers. Otherwise as msa_paged_attention_decode (same partitions and workspace);
+ * out has H * 128 columns. */
+int msa_paged_attention_decode_qkv(const uint16_t* qkv, int64_t ldqkv, const uint16_t* q_norm_w,
+                                   const uint16_t* k_norm_w, float qk_eps, const float* cos_table,
+                                   const float* sin_table, int64_t max_positions, const int64_t* slot_mapping,
+                                   uint16_t* k_cache,
+                                   uint16_t* v_cache, int64_t num_slots, int heads, int kv_heads, int head_dim,
+                                   int block_size, const int32_t* block_tables, int max_blocks,
+                                   const int32_t* context_lens, const int32_t* q_rows, int num_seqs,
+                                   int partition_tokens, int max_partitions, float scale, uint16_t* out,
+                                   int64_t ldo, void* workspace, size_t workspace_bytes, msa_stream_t stream);
+
 /* The prefill path of paged_attention (attention/backends.py:182-196) for chunks of any length,
  * fresh or continuing from cached keys: causal attention of each new token over positions
  * 0..its own, keys and values read through the block table from the caches (which already hold

@@ -166,6 +166,35 @@ def attend(q: Tensor, k_cache: Tensor, v_cache: Tensor, meta: AttentionMetadata,
     return out
 
 
+def attend_decode_qkv(
+    qkv: Tensor,
+    heads: int,
+    q_norm_w: Tensor,
+    k_norm_w: Tensor,
+    qk_eps: float,
+    cos_table: Tensor,
+    sin_table: Tensor,
+    k_cache: Tensor,
+    v_cache: Tensor,
+    meta: AttentionMetadata,
+    scale: float,
+) -> Tensor:
+    """A pure-decode step's attention from the qkv projection rows (model/qwen3.py:94-99): per-head
+    q/k RMSNorm, RoPE at each sequence's new position, the new keys and values written into the
+    caches at slot_mapping (negative slots are skipped) and attention, in one kernel. qkv [T, (H + 2 KVH) * D] -> [T, H, D]."""
+    if meta.decode is None or meta.prefill is not None:
+        raise RuntimeError("attend_decode_qkv serves batches of decode rows only")
+    d = meta.decode
+    kv_heads, dim = k_cache.shape[1], k_cache.shape[2]
+    out = torch.empty(qkv.shape[0], heads, dim, dtype=qkv.dtype, device=qkv.device)
+    ptok, parts = kernels.decode_splits(d.num_seqs, kv_heads, d.block_tables.shape[1])
+    kernels.paged_attention_decode_qkv(
+        qkv, heads, q_norm_w, k_norm_w, qk_eps, cos_table, sin_table, meta.slot_mapping, k_cache, v_cache, d.block_tables,
+        d.context_lens, d.q_rows, ptok, parts, scale, out, meta.block_size,
+    )
+    return out
+
+
 def paged_attention(
     q: Tensor,
     k: Tensor,

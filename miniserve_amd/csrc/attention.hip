@@ -42,6 +42,16 @@ struct DecodeArgs {
   int64_t ldo;
   float* ws_o;   // [num_seqs][heads][splits][128] unnormalized output of each split
   float* ws_ml;  // [num_seqs][heads][splits][2]   (running max, sum of exp) of each split
+  // Fused front half (the QKV template flag): q points at the projection rows [q | k | v] and the
+  // kernel applies the per-head RMSNorm and RoPE of model/qwen3.py:95-98 itself, writes the new
+  // token's key and value into the cache and attends to them from registers.
+  const uint16_t* qn_w;
+  const uint16_t* kn_w;
+  float qk_eps;
+  const float* cos_t;  // [max_pos, 128] float32
+  const float* sin_t;
+  int64_t max_pos;
+  const int64_t* slots;  // [T] cache slot of each row's new token (< 0: not written)
 };
 
 __device__ __forceinline__ void unpack8(const uint4& v, float (&f)[8]) {
@@ -98,7 +108,42 @@ __device__ __forceinline__ float rowpair_sum(float v) {
   return v;
 }
 
-template <int G, int W>
+// Per-head RMSNorm then RoPE (model/layers.py:18-22, 56-65 rounding) of the 16 dims this lane holds
+// -- [8dg, 8dg + 8) in v[0..3] and their rotary partners [64 + 8dg, 64 + 8dg + 8) in v[4..7], as
+// bf16 pairs -- given the norm weights of those dims and the float32 cos / sin of the position.
+// The sum of squares is completed over the 8 lanes of the lane's group (one head row).
+__device__ __forceinline__ void norm_rope16(uint32_t (&v)[8], const uint4& wlo, const uint4& whi, const float (&c)[16],
+                                            const float (&sn)[16], float eps) {
+  float x[16];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    x[2 * (e & 3) + 8 * (e >> 2)] = bf16lo(v[e]);
+    x[2 * (e & 3) + 1 + 8 * (e >> 2)] = bf16hi(v[e]);
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) ss += x[i] * x[i];
+  ss = group8_sum(ss);
+  const float r = 1.0f / sqrtf(ss / (float)kHeadDim + eps);
+  const uint32_t ww[8] = {wlo.x, wlo.y, wlo.z, wlo.w, whi.x, whi.y, whi.z, whi.w};
+  float y[16];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    y[2 * (e & 3) + 8 * (e >> 2)] = round_bf16(bf16lo(ww[e]) * round_bf16(x[2 * (e & 3) + 8 * (e >> 2)] * r));
+    y[2 * (e & 3) + 1 + 8 * (e >> 2)] = round_bf16(bf16hi(ww[e]) * round_bf16(x[2 * (e & 3) + 1 + 8 * (e >> 2)] * r));
+  }
+  float o[16];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {  // dim 8dg + i pairs with 64 + 8dg + i
+    const float x0 = y[i], x1 = y[8 + i];
+    o[i] = round_bf16(round_bf16(x0 * round_bf16(c[i])) + round_bf16(-x1 * round_bf16(sn[i])));
+    o[8 + i] = round_bf16(round_bf16(x1 * round_bf16(c[8 + i])) + round_bf16(x0 * round_bf16(sn[8 + i])));
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = pack_bf16x2(o[2 * (e & 3) + 8 * (e >> 2)], o[2 * (e & 3) + 1 + 8 * (e >> 2)]);
+}
+
+template <int G, int W, bool QKV>
 __global__ __launch_bounds__(64 * W) void paged_decode_kernel(DecodeArgs a) {
   __shared__ float s_acc[W][G][kHeadDim];
   __shared__ float s_ml[W][G][2];
@@ -127,6 +172,35 @@ __global__ __launch_bounds__(64 * W) void paged_decode_kernel(DecodeArgs a) {
     qv[h][0] = lo.x; qv[h][1] = lo.y; qv[h][2] = lo.z; qv[h][3] = lo.w;
     qv[h][4] = hi.x; qv[h][5] = hi.y; qv[h][6] = hi.z; qv[h][7] = hi.w;
   }
+  // Fused front half: the new token sits at position ctx - 1 (model_runner.py:186-189). Its key and
+  // value (this KV head) and the rotary tables of its position are loaded with q.
+  uint32_t kn[8], vn[8];
+  if constexpr (QKV) {
+    const uint16_t* kp = a.q + qrow * a.ldq + (int64_t)(a.heads + kvh) * kHeadDim + 8 * dg;
+    const uint16_t* vp = kp + (int64_t)a.kv_heads * kHeadDim;
+    const uint4 klo = *(const uint4*)kp, khi = *(const uint4*)(kp + 64);
+    const uint4 vlo = *(const uint4*)vp, vhi = *(const uint4*)(vp + 64);
+    kn[0] = klo.x; kn[1] = klo.y; kn[2] = klo.z; kn[3] = klo.w; kn[4] = khi.x; kn[5] = khi.y; kn[6] = khi.z; kn[7] = khi.w;
+    vn[0] = vlo.x; vn[1] = vlo.y; vn[2] = vlo.z; vn[3] = vlo.w; vn[4] = vhi.x; vn[5] = vhi.y; vn[6] = vhi.z; vn[7] = vhi.w;
+    const uint4 qwl = *(const uint4*)(a.qn_w + 8 * dg), qwh = *(const uint4*)(a.qn_w + 64 + 8 * dg);
+    const uint4 kwl = *(const uint4*)(a.kn_w + 8 * dg), kwh = *(const uint4*)(a.kn_w + 64 + 8 * dg);
+    int64_t pos = (int64_t)ctx - 1;
+    pos = pos < 0 ? 0 : (pos >= a.max_pos ? a.max_pos - 1 : pos);  // memory safety only
+    float c[16], sn[16];
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const float4* cp = (const float4*)(a.cos_t + pos * kHeadDim + 64 * hf + 8 * dg);
+      const float4* sp = (const float4*)(a.sin_t + pos * kHeadDim + 64 * hf + 8 * dg);
+      const float4 c0 = cp[0], c1 = cp[1], s0 = sp[0], s1 = sp[1];
+      c[8 * hf + 0] = c0.x; c[8 * hf + 1] = c0.y; c[8 * hf + 2] = c0.z; c[8 * hf + 3] = c0.w;
+      c[8 * hf + 4] = c1.x; c[8 * hf + 5] = c1.y; c[8 * hf + 6] = c1.z; c[8 * hf + 7] = c1.w;
+      sn[8 * hf + 0] = s0.x; sn[8 * hf + 1] = s0.y; sn[8 * hf + 2] = s0.z; sn[8 * hf + 3] = s0.w;
+      sn[8 * hf + 4] = s1.x; sn[8 * hf + 5] = s1.y; sn[8 * hf + 6] = s1.z; sn[8 * hf + 7] = s1.w;
+    }
+#pragma unroll
+    for (int h = 0; h < G; ++h) norm_rope16(qv[h], qwl, qwh, c, sn, a.qk_eps);
+    norm_rope16(kn, kwl, kwh, c, sn, a.qk_eps);
+  }
   float m[G], l[G], acc[G][16];
 #pragma unroll
   for (int h = 0; h < G; ++h) {
@@ -151,7 +225,8 @@ __global__ __launch_bounds__(64 * W) void paged_decode_kernel(DecodeArgs a) {
   uint4 ka[2][2], va[2][2], kb[2][2], vb[2][2];
   if (bfirst < a.max_blocks) load_block(ph0, ka, va);  // before the context length is known
   if (start >= ctx) return;  // the reduce kernel merges only splits that hold keys
-  const int end = min(ctx, start + a.part_tokens);
+  // Fused: the cache is read for the keys before the new token, which comes from registers.
+  const int end = min(QKV ? ctx - 1 : ctx, start + a.part_tokens);
   const int b1 = (end + kBlock - 1) / kBlock;
 
   // One block of q.k, online softmax and p.v on K/V registers kr, vr (wave-uniform block index).
@@ -226,6 +301,50 @@ __global__ __launch_bounds__(64 * W) void paged_decode_kernel(DecodeArgs a) {
     process(b, kb, vb);
     b += W;
     ph_next = ph_b;
+  }
+  if constexpr (QKV) {
+    // The new token: wavefront 0 of the split holding position ctx - 1 attends to it (row 0 of
+    // its lanes' first row pair only) and writes its key and value into the cache.
+    if (wave == 0 && ctx - 1 < start + a.part_tokens) {
+      float sc[G];
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        float d = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) d = dot2(kn[e], qv[h][e], d);
+        sc[h] = group8_sum(d) * a.scale_log2;  // the same in every row pair
+      }
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        if (sc[h] > m[h]) {  // wave-uniform
+          const float alpha = exp2f(m[h] - sc[h]);
+          m[h] = sc[h];
+          l[h] *= alpha;
+#pragma unroll
+          for (int e = 0; e < 16; ++e) acc[h][e] *= alpha;
+        }
+        if (rp == 0) {
+          const float p = round_bf16(exp2f(sc[h] - m[h]));
+          l[h] += p;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {  // acc[h][e]: dim 8dg + e (e < 8), 64 + 8dg + e - 8 (e >= 8)
+            const int x = 2 * (e & 3) + 8 * (e >> 2);
+            acc[h][x] += bf16lo(vn[e]) * p;
+            acc[h][x + 1] += bf16hi(vn[e]) * p;
+          }
+        }
+      }
+      if (rp == 0) {
+        const int64_t slot = a.slots[qrow];
+        if (slot >= 0 && slot < a.num_blocks * kBlock) {
+          const int64_t off = slot * tok_stride + (int64_t)kvh * kHeadDim + 8 * dg;
+          *(uint4*)(const_cast<uint16_t*>(a.kc) + off) = uint4{kn[0], kn[1], kn[2], kn[3]};
+          *(uint4*)(const_cast<uint16_t*>(a.kc) + off + 64) = uint4{kn[4], kn[5], kn[6], kn[7]};
+          *(uint4*)(const_cast<uint16_t*>(a.vc) + off) = uint4{vn[0], vn[1], vn[2], vn[3]};
+          *(uint4*)(const_cast<uint16_t*>(a.vc) + off + 64) = uint4{vn[4], vn[5], vn[6], vn[7]};
+        }
+      }
+    }
   }
   // Merge the row pairs of the wavefront (lanes dg, dg + 8, ...), then the wavefronts through LDS.
   // acc[h][e]: dim 8dg + e for e < 8, 64 + 8dg + (e - 8) for e >= 8.
@@ -490,14 +609,49 @@ extern "C" size_t msa_paged_attention_decode_workspace_size(int num_seqs, int he
 }
 
 namespace msa {
-template <int G>
+template <int G, bool QKV = false>
 static void launch_decode(const DecodeArgs& a, int num_seqs, hipStream_t s) {
   // Four wavefronts per workgroup: at the kernel's register count (three wavefronts per SIMD for
   // G <= 2) three workgroups share a CU, so a batch's (sequence, KV head) pairs are resident at
   // once.
   constexpr int W = 4;
   const dim3 grid(a.kv_heads, a.splits, num_seqs);
-  hipLaunchKernelGGL((paged_decode_kernel<G, W>), grid, dim3(64 * W), 0, s, a);
+  hipLaunchKernelGGL((paged_decode_kernel<G, W, QKV>), grid, dim3(64 * W), 0, s, a);
+}
+
+// Shared checks and workspace binding of the two decode entry points.
+static int decode_args(const char* who, const uint16_t* q, int64_t ldq, const uint16_t* k_cache, const uint16_t* v_cache,
+                       int64_t num_slots, int heads, int kv_heads, int head_dim, int block_size,
+                       const int32_t* block_tables, int max_blocks, const int32_t* context_lens, const int32_t* q_rows,
+                       int num_seqs, int partition_tokens, int max_partitions, float scale, uint16_t* out, int64_t ldo,
+                       void* workspace, size_t workspace_bytes, DecodeArgs& a) {
+  const std::string w(who);
+  if (!q || !k_cache || !v_cache || !block_tables || !context_lens || !q_rows || !out)
+    return fail(MSA_ERR_INVALID, w + ": null pointer");
+  if (head_dim != kHeadDim) return fail(MSA_ERR_UNSUPPORTED, w + ": head_dim must be 128");
+  if (block_size != kBlock) return fail(MSA_ERR_UNSUPPORTED, w + ": block_size must be 16");
+  if (num_seqs < 0 || num_seqs > 65535 || heads <= 0 || kv_heads <= 0 || heads % kv_heads != 0 || max_blocks <= 0)
+    return fail(MSA_ERR_INVALID, w + ": bad shape (num_seqs <= 65535)");
+  if (partition_tokens <= 0 || partition_tokens % kBlock != 0 || max_partitions <= 0 || max_partitions > 65535)
+    return fail(MSA_ERR_INVALID, w + ": partition_tokens must be a positive multiple of 16");
+  if ((int64_t)partition_tokens * max_partitions < (int64_t)max_blocks * kBlock)
+    return fail(MSA_ERR_INVALID, w + ": partition_tokens * max_partitions must cover max_blocks * 16");
+  if (ldq % 8 != 0 || !aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out))
+    return fail(MSA_ERR_INVALID, w + ": q/out/caches must be 16-byte aligned");
+  a = DecodeArgs{};
+  a.q = q; a.ldq = ldq; a.kc = k_cache; a.vc = v_cache; a.num_blocks = num_slots / kBlock;
+  a.heads = heads; a.kv_heads = kv_heads; a.bt = block_tables; a.max_blocks = max_blocks;
+  a.ctx = context_lens; a.qrows = q_rows; a.part_tokens = partition_tokens; a.splits = max_partitions;
+  a.scale_log2 = scale * kLog2e; a.out = out; a.ldo = ldo;
+  if (max_partitions > 1) {
+    const size_t need = msa_paged_attention_decode_workspace_size(num_seqs, heads, head_dim, max_partitions);
+    if (!workspace || workspace_bytes < need) return fail(MSA_ERR_WORKSPACE, w + ": workspace smaller than the workspace size");
+    if (!aligned16(workspace)) return fail(MSA_ERR_INVALID, w + ": workspace must be 16-byte aligned");
+    const size_t slots = (size_t)num_seqs * heads * max_partitions;
+    a.ws_o = (float*)workspace;
+    a.ws_ml = a.ws_o + slots * head_dim;
+  }
+  return MSA_OK;
 }
 }  // namespace msa
 
@@ -509,32 +663,11 @@ extern "C" int msa_paged_attention_decode(const uint16_t* q, int64_t ldq, const 
                                           size_t workspace_bytes, msa_stream_t stream) {
   using namespace msa;
   if (num_seqs == 0) return MSA_OK;
-  if (!q || !k_cache || !v_cache || !block_tables || !context_lens || !q_rows || !out)
-    return fail(MSA_ERR_INVALID, "msa_paged_attention_decode: null pointer");
-  if (head_dim != kHeadDim) return fail(MSA_ERR_UNSUPPORTED, "msa_paged_attention_decode: head_dim must be 128");
-  if (block_size != kBlock) return fail(MSA_ERR_UNSUPPORTED, "msa_paged_attention_decode: block_size must be 16");
-  if (num_seqs < 0 || num_seqs > 65535 || heads <= 0 || kv_heads <= 0 || heads % kv_heads != 0 || max_blocks <= 0)
-    return fail(MSA_ERR_INVALID, "msa_paged_attention_decode: bad shape (num_seqs <= 65535)");
-  if (partition_tokens <= 0 || partition_tokens % kBlock != 0 || max_partitions <= 0 || max_partitions > 65535)
-    return fail(MSA_ERR_INVALID, "msa_paged_attention_decode: partition_tokens must be a positive multiple of 16");
-  if ((int64_t)partition_tokens * max_partitions < (int64_t)max_blocks * kBlock)
-    return fail(MSA_ERR_INVALID, "msa_paged_attention_decode: partition_tokens * max_partitions must cover max_blocks * 16");
-  if (ldq % 8 != 0 || !aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out))
-    return fail(MSA_ERR_INVALID, "msa_paged_attention_decode: q/out/caches must be 16-byte aligned");
-  DecodeArgs a{};
-  a.q = q; a.ldq = ldq; a.kc = k_cache; a.vc = v_cache; a.num_blocks = num_slots / kBlock;
-  a.heads = heads; a.kv_heads = kv_heads; a.bt = block_tables; a.max_blocks = max_blocks;
-  a.ctx = context_lens; a.qrows = q_rows; a.part_tokens = partition_tokens; a.splits = max_partitions;
-  a.scale_log2 = scale * kLog2e; a.out = out; a.ldo = ldo;
-  if (max_partitions > 1) {
-    const size_t need = msa_paged_attention_decode_workspace_size(num_seqs, heads, head_dim, max_partitions);
-    if (!workspace || workspace_bytes < need)
-      return fail(MSA_ERR_WORKSPACE, "msa_paged_attention_decode: workspace smaller than the workspace size");
-    if (!aligned16(workspace)) return fail(MSA_ERR_INVALID, "msa_paged_attention_decode: workspace must be 16-byte aligned");
-    const size_t slots = (size_t)num_seqs * heads * max_partitions;
-    a.ws_o = (float*)workspace;
-    a.ws_ml = a.ws_o + slots * head_dim;
-  }
+  DecodeArgs a;
+  int rc = decode_args("msa_paged_attention_decode", q, ldq, k_cache, v_cache, num_slots, heads, kv_heads, head_dim,
+                       block_size, block_tables, max_blocks, context_lens, q_rows, num_seqs, partition_tokens,
+                       max_partitions, scale, out, ldo, workspace, workspace_bytes, a);
+  if (rc != MSA_OK) return rc;
   hipStream_t s = (hipStream_t)stream;
   switch (heads / kv_heads) {
     case 1: launch_decode<1>(a, num_seqs, s); break;
@@ -543,10 +676,50 @@ extern "C" int msa_paged_attention_decode(const uint16_t* q, int64_t ldq, const 
     case 8: launch_decode<8>(a, num_seqs, s); break;
     default: return fail(MSA_ERR_UNSUPPORTED, "msa_paged_attention_decode: heads / kv_heads must be 1, 2, 4 or 8");
   }
-  int rc = check_launch("msa_paged_attention_decode");
+  rc = check_launch("msa_paged_attention_decode");
   if (rc != MSA_OK || max_partitions == 1) return rc;
   hipLaunchKernelGGL(paged_decode_reduce_kernel, dim3(num_seqs, heads), dim3(kHeadDim), 0, s, a);
   return check_launch("msa_paged_attention_decode (split merge)");
+}
+
+extern "C" int msa_paged_attention_decode_qkv(const uint16_t* qkv, int64_t ldqkv, const uint16_t* q_norm_w,
+                                              const uint16_t* k_norm_w, float qk_eps, const float* cos_table,
+                                              const float* sin_table, int64_t max_positions,
+                                              const int64_t* slot_mapping, uint16_t* k_cache,
+                                              uint16_t* v_cache, int64_t num_slots, int heads, int kv_heads,
+                                              int head_dim, int block_size, const int32_t* block_tables,
+                                              int max_blocks, const int32_t* context_lens, const int32_t* q_rows,
+                                              int num_seqs, int partition_tokens, int max_partitions, float scale,
+                                              uint16_t* out, int64_t ldo, void* workspace, size_t workspace_bytes,
+                                              msa_stream_t stream) {
+  using namespace msa;
+  if (num_seqs == 0) return MSA_OK;
+  DecodeArgs a;
+  int rc = decode_args("msa_paged_attention_decode_qkv", qkv, ldqkv, k_cache, v_cache, num_slots, heads, kv_heads,
+                       head_dim, block_size, block_tables, max_blocks, context_lens, q_rows, num_seqs, partition_tokens,
+                       max_partitions, scale, out, ldo, workspace, workspace_bytes, a);
+  if (rc != MSA_OK) return rc;
+  if (!q_norm_w || !k_norm_w || !cos_table || !sin_table || !slot_mapping || max_positions <= 0)
+    return fail(MSA_ERR_INVALID, "msa_paged_attention_decode_qkv: null norm weight / rotary table / slot_mapping");
+  if (!aligned16(q_norm_w) || !aligned16(k_norm_w) || !aligned16(cos_table) || !aligned16(sin_table))
+    return fail(MSA_ERR_INVALID, "msa_paged_attention_decode_qkv: norm weights / rotary tables must be 16-byte aligned");
+  if (ldqkv < (int64_t)(heads + 2 * kv_heads) * kHeadDim)
+    return fail(MSA_ERR_INVALID, "msa_paged_attention_decode_qkv: ldqkv smaller than (heads + 2 kv_heads) * 128");
+  a.qn_w = q_norm_w; a.kn_w = k_norm_w; a.qk_eps = qk_eps; a.cos_t = cos_table; a.sin_t = sin_table;
+  a.max_pos = max_positions;
+  a.slots = slot_mapping;
+  hipStream_t s = (hipStream_t)stream;
+  switch (heads / kv_heads) {
+    case 1: launch_decode<1, true>(a, num_seqs, s); break;
+    case 2: launch_decode<2, true>(a, num_seqs, s); break;
+    case 4: launch_decode<4, true>(a, num_seqs, s); break;
+    case 8: launch_decode<8, true>(a, num_seqs, s); break;
+    default: return fail(MSA_ERR_UNSUPPORTED, "msa_paged_attention_decode_qkv: heads / kv_heads must be 1, 2, 4 or 8");
+  }
+  rc = check_launch("msa_paged_attention_decode_qkv");
+  if (rc != MSA_OK || max_partitions == 1) return rc;
+  hipLaunchKernelGGL(paged_decode_reduce_kernel, dim3(num_seqs, heads), dim3(kHeadDim), 0, s, a);
+  return check_launch("msa_paged_attention_decode_qkv (split merge)");
 }
 
 extern "C" int msa_paged_attention_prefill(const uint16_t* q, int64_t ldq, const uint16_t* k_cache,

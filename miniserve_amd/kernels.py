@@ -325,6 +325,57 @@ def paged_attention_decode(
     return out
 
 
+def paged_attention_decode_qkv(
+    qkv: Tensor,
+    heads: int,
+    q_norm_w: Tensor,
+    k_norm_w: Tensor,
+    qk_eps: float,
+    cos_table: Tensor,
+    sin_table: Tensor,
+    slot_mapping: Tensor,
+    k_cache: Tensor,
+    v_cache: Tensor,
+    block_tables: Tensor,
+    context_lens: Tensor,
+    q_rows: Tensor,
+    partition_tokens: int,
+    max_partitions: int,
+    scale: float,
+    out: Tensor,
+    block_size: int = 16,
+) -> Tensor:
+    """Decode attention from the qkv projection rows [q | k | v] (msa_paged_attention_decode_qkv):
+    per-head q/k RMSNorm and RoPE at position context_len - 1, the new key and value written into
+    the caches at slot_mapping (negative slots are skipped), attention over the cached keys plus
+    the new one. out [T, heads, head_dim]."""
+    _on_gpu(qkv, q_norm_w, k_norm_w, cos_table, sin_table, slot_mapping, k_cache, v_cache, block_tables, context_lens,
+            q_rows, out)
+    _check(slot_mapping.dtype == torch.int64 and slot_mapping.numel() == qkv.shape[0], "paged_attention_decode_qkv: slots")
+    _, kvh, d = k_cache.shape
+    _check(qkv.dtype == torch.bfloat16 and qkv.dim() == 2 and qkv.stride(-1) == 1
+           and qkv.shape[1] == (heads + 2 * kvh) * d, "paged_attention_decode_qkv: qkv [T, (H + 2 KVH) * D]")
+    _check(cos_table.dtype == torch.float32 and cos_table.is_contiguous() and cos_table.shape[-1] == d
+           and sin_table.shape == cos_table.shape and sin_table.is_contiguous(), "paged_attention_decode_qkv: rotary")
+    _check(k_cache.is_contiguous() and v_cache.is_contiguous(), "paged_attention_decode_qkv: caches")
+    num = context_lens.numel()
+    _check(block_tables.dtype == torch.int32 and block_tables.is_contiguous() and block_tables.shape[0] == num,
+           "paged_attention_decode_qkv: block_tables")
+    _check(context_lens.dtype == torch.int32 and q_rows.dtype == torch.int32, "paged_attention_decode_qkv: metadata")
+    ws_bytes = _native.query("msa_paged_attention_decode_workspace_size", num, heads, d, max_partitions)
+    ws = workspaces.get("attention", qkv.device, ws_bytes)
+    o2 = out.view(out.shape[0], -1)
+    _native.call(
+        "msa_paged_attention_decode_qkv", _ptr(qkv), qkv.stride(0), _ptr(q_norm_w), _ptr(k_norm_w), float(qk_eps),
+        _ptr(cos_table), _ptr(sin_table), cos_table.shape[0], _ptr(slot_mapping), _ptr(k_cache), _ptr(v_cache),
+        k_cache.shape[0], heads,
+        kvh, d, block_size, _ptr(block_tables), block_tables.shape[1], _ptr(context_lens), _ptr(q_rows), num,
+        partition_tokens, max_partitions, float(scale), _ptr(o2), o2.stride(0), _ptr(ws),
+        ws.numel() if ws is not None else 0, _stream(qkv),
+    )
+    return out
+
+
 def paged_attention_prefill(
     q: Tensor,
     k_cache: Tensor,

@@ -28,7 +28,7 @@ import torch.nn.functional as F
 from torch import Tensor, nn
 
 from miniserve_amd import kernels
-from miniserve_amd.attention.backends import AttentionMetadata, attend
+from miniserve_amd.attention.backends import AttentionMetadata, attend, attend_decode_qkv
 from miniserve_amd.model.layers import RMSNorm, RotaryEmbedding, SwiGLU
 from miniserve_amd.quant.int8 import Int8Linear
 
@@ -235,17 +235,35 @@ class Qwen3ForCausalLM(nn.Module):
                 return kernels.int8_linear_dec
             return kernels.int8_linear_rows
 
+        # Pure-decode batches: the qkv projection as a plain decode linear and the per-head norms,
+        # RoPE and KV write inside the decode attention kernel.
+        fused_decode = (
+            meta.prefill is None and meta.decode is not None and t <= kernels.DEC_MAX_TOKENS
+            and kernels.dec_supported(cfg.hidden_size)
+        )
         for i, (layer, (k_cache, v_cache)) in enumerate(zip(self.layers, kv_caches, strict=True)):
             attn, mlp = layer.self_attn, layer.mlp
             qkv, o, gu, dn = attn.qkv_proj, attn.o_proj, mlp.gate_up_proj, mlp.down_proj
             first = i == 0
-            q = kernels.qkv_rope_cache_rows(
-                self.embed_tokens.weight if first else residual, qkv.qweight, qkv.scale, attn.num_heads,
-                attn.num_kv_heads, attn.head_dim, attn.q_norm.weight, attn.k_norm.weight, attn.q_norm.eps, pos,
-                rot.cos, rot.sin, meta.slot_mapping, k_cache, v_cache, norm_w=layer.input_layernorm.weight,
-                eps=layer.input_layernorm.eps, gather=ids if first else None, x_copy=residual if first else None,
-            )
-            a = attend(q, k_cache, v_cache, meta, attn.scale).view(t, attn.q_size)
+            src = self.embed_tokens.weight if first else residual
+            if fused_decode:
+                # [gather + input RMSNorm + int8 qkv] -> [q/k-norm + RoPE + KV write + attention]
+                qkv_rows = kernels.int8_linear_dec(
+                    src, qkv.qweight, qkv.scale, norm_w=layer.input_layernorm.weight, eps=layer.input_layernorm.eps,
+                    gather=ids if first else None, x_copy=residual if first else None,
+                )
+                a = attend_decode_qkv(
+                    qkv_rows, attn.num_heads, attn.q_norm.weight, attn.k_norm.weight, attn.q_norm.eps, rot.cos,
+                    rot.sin, k_cache, v_cache, meta, attn.scale,
+                ).view(t, attn.q_size)
+            else:
+                q = kernels.qkv_rope_cache_rows(
+                    src, qkv.qweight, qkv.scale, attn.num_heads, attn.num_kv_heads, attn.head_dim,
+                    attn.q_norm.weight, attn.k_norm.weight, attn.q_norm.eps, pos, rot.cos, rot.sin,
+                    meta.slot_mapping, k_cache, v_cache, norm_w=layer.input_layernorm.weight,
+                    eps=layer.input_layernorm.eps, gather=ids if first else None, x_copy=residual if first else None,
+                )
+                a = attend(q, k_cache, v_cache, meta, attn.scale).view(t, attn.q_size)
             lin(attn.q_size)(a, o.qweight, o.scale, kernels.EPI_RESIDUAL, residual=residual, out=residual)
             act = lin(cfg.hidden_size)(
                 residual, gu.qweight, gu.scale, kernels.EPI_SILU_MUL,

@@ -360,3 +360,82 @@ def test_decode_attention_split_across_workgroups(heads, kv_heads, ptok):
                                        scale, out)
         assert rel_l2(out.cpu(), ref) < 1e-2
     assert kernels.decode_splits(2, 8, 256)[1] > 1  # the host picks splits for small batches
+
+
+@pytest.mark.parametrize("heads,kv_heads,ptok", [(16, 8, 0), (32, 8, 0), (8, 8, 0), (16, 8, 32), (16, 4, 64)])
+def test_decode_attention_from_qkv(heads, kv_heads, ptok):
+    """msa_paged_attention_decode_qkv -- per-head q/k RMSNorm, RoPE at position context - 1, the new
+    key / value written into the caches, attention over the cached keys plus the new one -- against
+    the oracle's layer sequence (model/qwen3.py:95-99, attention/backends.py:145-180) on the same
+    projection rows, and against the unfused HIP kernels. ptok > 0 splits each sequence's keys over
+    workgroups of ptok keys."""
+    dim, scale = 128, 128**-0.5
+    rng = random.Random(heads + 7 * kv_heads + ptok)
+    specs = [(rng.randint(0, 700), 1) for _ in range(23)] + [(0, 1), (15, 1), (16, 1), (31, 1), (32, 1), (2047, 1)]
+    _, _, _, kc, vc, chunks, slots = _attention_case(specs, heads, kv_heads, seed=heads + ptok + 3)
+    t = len(specs)
+    qkv = _bf16((t, (heads + 2 * kv_heads) * dim), seed=heads + 11)
+    gen = torch.Generator().manual_seed(heads + 13)
+    qw = (1 + 0.1 * torch.randn(dim, generator=gen)).to(torch.bfloat16)
+    kw = (1 + 0.1 * torch.randn(dim, generator=gen)).to(torch.bfloat16)
+    cos_t, sin_t = ol.rope_tables(dim, 4096, 1e6)
+    pos = torch.tensor([c[2] for c in chunks])  # a decode token sits at position num_cached
+    # oracle: norms, RoPE, cache write, attention
+    qr, kr, vr = qkv.split([heads * dim, kv_heads * dim, kv_heads * dim], dim=-1)
+    qn = ol.rms_norm(qr.reshape(t, heads, dim), qw, 1e-6)
+    kn = ol.rms_norm(kr.reshape(t, kv_heads, dim), kw, 1e-6)
+    qo, ko = ol.apply_rope(qn, kn, cos_t[pos], sin_t[pos])
+    seqs = [oa.SeqChunk(*c) for c in chunks]
+    kco, vco = kc.clone(), vc.clone()
+    ref = oa.paged_attention(qo, ko, vr.reshape(t, kv_heads, dim), kco, vco, oa.build_attention_metadata(seqs, slots, 16),
+                             scale)
+    dense = oa.dense_attention(qo, kco, vco, seqs, 16, scale)
+    # fused HIP kernel
+    hmeta = hb.build_attention_metadata([hb.SeqChunk(*c) for c in chunks], slots.to(DEV), 16)
+    kcg, vcg = kc.to(DEV), vc.to(DEV)
+    args = (qkv.to(DEV), heads, qw.to(DEV), kw.to(DEV), 1e-6, cos_t.to(DEV), sin_t.to(DEV))
+    cache_args = (kcg, vcg)
+    if ptok:
+        d = hmeta.decode
+        parts = -(-d.block_tables.shape[1] * 16 // ptok)
+        out = torch.empty(t, heads, dim, dtype=torch.bfloat16, device=DEV)
+        kernels.paged_attention_decode_qkv(*args, slots.to(DEV), *cache_args, d.block_tables, d.context_lens, d.q_rows,
+                                           ptok, parts, scale, out)
+    else:
+        out = hb.attend_decode_qkv(*args, *cache_args, hmeta, scale)
+    out = out.cpu()
+    assert rel_l2(out, ref) < 1e-2
+    assert rel_l2(out, dense) < 1e-2
+    # the cache writes: values bit-exact, keys as the norm + RoPE bar, every other slot untouched
+    kmag = kn.float().abs() + torch.cat([kn[..., dim // 2 :], kn[..., : dim // 2]], -1).float().abs()
+    kcc, vcc = kcg.cpu(), vcg.cpu()
+    assert torch.equal(vcc, vco)
+    _close_bf16(kcc[slots], kco[slots], scale=kmag)
+    others = torch.ones(kc.shape[0], dtype=torch.bool)
+    others[slots] = False
+    assert torch.equal(kcc[others], kc[others])
+    # against the unfused kernels: qk_norm_rope_cache, then decode attention
+    kc2, vc2 = kc.to(DEV), vc.to(DEV)
+    q2 = kernels.qk_norm_rope_cache(qkv.to(DEV), heads, kv_heads, dim, qw.to(DEV), kw.to(DEV), 1e-6,
+                                    cos_t[pos].to(DEV), sin_t[pos].to(DEV), slots.to(DEV), kc2, vc2)
+    out2 = hb.attend(q2, kc2, vc2, hmeta, scale).cpu()
+    assert torch.equal(vc2.cpu(), vcc)
+    _close_bf16(kcc[slots], kc2.cpu()[slots], scale=kmag)
+    assert rel_l2(out, out2) < 2e-3
+
+
+def test_decode_attention_from_qkv_skips_negative_slots():
+    """Rows whose slot is negative (a captured graph's warm-up rows) write nothing; their attention
+    is still computed (over the cached keys and the new key from registers)."""
+    heads, kv_heads, dim, scale = 16, 8, 128, 128**-0.5
+    specs = [(40, 1), (0, 1), (16, 1), (300, 1)]
+    _, _, _, kc, vc, chunks, slots = _attention_case(specs, heads, kv_heads, seed=5)
+    qkv = _bf16((len(specs), (heads + 2 * kv_heads) * dim), seed=6)
+    w = torch.ones(dim, dtype=torch.bfloat16, device=DEV)
+    cos_t, sin_t = ol.rope_tables(dim, 4096, 1e6)
+    neg = torch.full_like(slots, -1)
+    hmeta = hb.build_attention_metadata([hb.SeqChunk(*c) for c in chunks], neg.to(DEV), 16)
+    kcg, vcg = kc.to(DEV), vc.to(DEV)
+    out = hb.attend_decode_qkv(qkv.to(DEV), heads, w, w, 1e-6, cos_t.to(DEV), sin_t.to(DEV), kcg, vcg, hmeta, scale)
+    assert torch.equal(kcg.cpu(), kc) and torch.equal(vcg.cpu(), vc)
+    assert bool(torch.isfinite(out.float()).all())

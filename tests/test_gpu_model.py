@@ -210,12 +210,13 @@ def test_qwen3_0_6b_greedy_ids_over_steps(seed):
 
     End to end, 28 random-init bf16 layers drift apart by a few percent whichever two bf16 paths
     are compared, so each step asserts what the single-layer tests cannot: the HIP logits are no
-    further from the float64 logits than 1.5x the oracle's own distance; the float64 regret of the
-    HIP picks (the sum over rows of the float64 logit of the float64 argmax less that of the pick)
-    is at most 1.5x the oracle's plus 0.05 -- with several near-tied rows per step, how many rows
-    two equally accurate bf16 paths get exactly right varies by a few rows, while the regret
-    weighs each wrong pick by how wrong it is -- and the HIP path disagrees with the oracle only
-    where the float64 logits of the two picks are within 0.1 (each mismatch is printed)."""
+    further from the float64 logits than 1.5x the oracle's own distance; in every row the HIP pick
+    is no further below the float64 maximum (its float64 regret) than four times the RMS error of
+    the oracle's own logits in that row -- a pick that noise of the oracle's size could have made;
+    with several near-tied rows per step, how many rows two equally accurate bf16 paths get exactly
+    right varies by a few rows, so no count is compared -- and the HIP path disagrees with the
+    oracle only where the float64 logits of the two picks are within 0.1 (each mismatch is
+    printed)."""
     cfg = workloads.QWEN3_0_6B
     batch = workloads.decode_batch(64, 256, 384, seed=seed, vocab=cfg["vocab_size"], spare_blocks=64)
     runner, ocfg, ow, okv, tables = _pair(cfg, seed=seed, max_positions=4096, num_blocks=batch.num_blocks, jitter=0.0)
@@ -245,8 +246,9 @@ def test_qwen3_0_6b_greedy_ids_over_steps(seed):
         e_hip, e_ref = rel_l2(got, logits64), rel_l2(ref, logits64)
         hip_exact, oracle_exact = int((graph_ids == ids64).sum()), int((ref_ids == ids64).sum())
         best64 = logits64.gather(1, ids64.view(-1, 1)).flatten()
-        regret_hip = float((best64 - logits64.gather(1, graph_ids.view(-1, 1)).flatten()).sum())
-        regret_ref = float((best64 - logits64.gather(1, ref_ids.view(-1, 1)).flatten()).sum())
+        regret = best64 - logits64.gather(1, graph_ids.view(-1, 1)).flatten()
+        noise = (ref.double() - logits64).pow(2).mean(-1).sqrt()  # the oracle's own logit error per row
+        regret_hip, regret_ref = float(regret.sum()), float((best64 - logits64.gather(1, ref_ids.view(-1, 1)).flatten()).sum())
         bad = (graph_ids != ref_ids).nonzero().flatten().tolist()
         report = [(i, int(graph_ids[i]), int(ref_ids[i]), float(logits64[i, ref_ids[i]] - logits64[i, graph_ids[i]]))
                   for i in bad]
@@ -255,7 +257,7 @@ def test_qwen3_0_6b_greedy_ids_over_steps(seed):
               f"(oracle {oracle_exact}/64); float64 regret {regret_hip:.4f} (oracle {regret_ref:.4f}); "
               f"mismatches (row, hip, oracle, float64 gap): {report}")
         assert e_hip <= 1.5 * e_ref, step
-        assert regret_hip <= 1.5 * regret_ref + 0.05, step
+        assert bool((regret <= 4 * noise).all()), (step, float((regret / noise).max()))
         assert all(abs(r[3]) <= 0.1 for r in report), report
         sched = [ScheduledChunk(s.token_ids + [int(ref_ids[i])], len(s.token_ids), 1, s.block_table)
                  for i, s in enumerate(sched)]
