@@ -42,8 +42,6 @@ METRIC = "decode tok/s at batch 64 (Qwen3-0.6B int8); int8 GEMV + attn HBM GB/s 
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 BATCH, CTX_LO, CTX_HI = 64, 256, 384
-# FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 of one decode-attention launch on the decode workload, from
-# rocprofv3 --pmc: 42,618.69 KiB x 2 x 1024 + 256 KiB x 1024 (profiles/paged_decode_kernel_traffic_pmc.md).
 # FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 of one fused decode-attention launch on the decode workload,
 # from rocprofv3 --pmc: 42,902.07 KiB x 2 x 1024 + 512 KiB x 1024
 # (profiles/paged_decode_kernel_traffic_pmc.md).

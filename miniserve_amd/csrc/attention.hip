@@ -165,25 +165,22 @@ __global__ __launch_bounds__(64 * W) void paged_decode_kernel(DecodeArgs a) {
 
   // q of this lane's 16 dims for each head of the group, as bf16 pairs
   uint32_t qv[G][8];
+  uint32_t kn[8], vn[8];  // fused: the new token's key (normed, rotated) and value, this KV head
+  auto load8 = [&](const uint16_t* p, uint32_t (&v)[8]) {
+    const uint4 lo = *(const uint4*)p, hi = *(const uint4*)(p + 64);
+    v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w;
+    v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
+  };
+  const uint16_t* qrow_p = a.q + qrow * a.ldq;
+  if constexpr (!QKV) {
 #pragma unroll
-  for (int h = 0; h < G; ++h) {
-    const uint16_t* qp = a.q + qrow * a.ldq + (int64_t)(kvh * G + h) * kHeadDim + 8 * dg;
-    const uint4 lo = *(const uint4*)qp, hi = *(const uint4*)(qp + 64);
-    qv[h][0] = lo.x; qv[h][1] = lo.y; qv[h][2] = lo.z; qv[h][3] = lo.w;
-    qv[h][4] = hi.x; qv[h][5] = hi.y; qv[h][6] = hi.z; qv[h][7] = hi.w;
-  }
-  // Fused front half: the new token sits at position ctx - 1 (model_runner.py:186-189). Its key and
-  // value (this KV head) and the rotary tables of its position are loaded with q.
-  uint32_t kn[8], vn[8];
-  if constexpr (QKV) {
-    const uint16_t* kp = a.q + qrow * a.ldq + (int64_t)(a.heads + kvh) * kHeadDim + 8 * dg;
-    const uint16_t* vp = kp + (int64_t)a.kv_heads * kHeadDim;
-    const uint4 klo = *(const uint4*)kp, khi = *(const uint4*)(kp + 64);
-    const uint4 vlo = *(const uint4*)vp, vhi = *(const uint4*)(vp + 64);
-    kn[0] = klo.x; kn[1] = klo.y; kn[2] = klo.z; kn[3] = klo.w; kn[4] = khi.x; kn[5] = khi.y; kn[6] = khi.z; kn[7] = khi.w;
-    vn[0] = vlo.x; vn[1] = vlo.y; vn[2] = vlo.z; vn[3] = vlo.w; vn[4] = vhi.x; vn[5] = vhi.y; vn[6] = vhi.z; vn[7] = vhi.w;
-    const uint4 qwl = *(const uint4*)(a.qn_w + 8 * dg), qwh = *(const uint4*)(a.qn_w + 64 + 8 * dg);
-    const uint4 kwl = *(const uint4*)(a.kn_w + 8 * dg), kwh = *(const uint4*)(a.kn_w + 64 + 8 * dg);
+    for (int h = 0; h < G; ++h) load8(qrow_p + (int64_t)(kvh * G + h) * kHeadDim + 8 * dg, qv[h]);
+  } else {
+    // Fused front half: the new token sits at position ctx - 1 (model_runner.py:186-189). The G
+    // query heads and the key are normed and rotated once per workgroup lane group: vector v of
+    // the G + 1 is done by the row-pair group rp == v (of its round), then every lane gathers
+    // all of them from those groups' lanes with the same dims.
+    load8(qrow_p + (int64_t)(a.heads + a.kv_heads + kvh) * kHeadDim + 8 * dg, vn);
     int64_t pos = (int64_t)ctx - 1;
     pos = pos < 0 ? 0 : (pos >= a.max_pos ? a.max_pos - 1 : pos);  // memory safety only
     float c[16], sn[16];
@@ -197,9 +194,25 @@ __global__ __launch_bounds__(64 * W) void paged_decode_kernel(DecodeArgs a) {
       sn[8 * hf + 0] = s0.x; sn[8 * hf + 1] = s0.y; sn[8 * hf + 2] = s0.z; sn[8 * hf + 3] = s0.w;
       sn[8 * hf + 4] = s1.x; sn[8 * hf + 5] = s1.y; sn[8 * hf + 6] = s1.z; sn[8 * hf + 7] = s1.w;
     }
+    constexpr int kRounds = (G + 1 + 7) / 8;
 #pragma unroll
-    for (int h = 0; h < G; ++h) norm_rope16(qv[h], qwl, qwh, c, sn, a.qk_eps);
-    norm_rope16(kn, kwl, kwh, c, sn, a.qk_eps);
+    for (int round = 0; round < kRounds; ++round) {
+      const int vi = min(round * 8 + rp, G);  // groups past the last vector redo the key (unused)
+      const bool is_k = vi == G;
+      uint32_t mine[8];
+      load8(qrow_p + (int64_t)(is_k ? a.heads + kvh : kvh * G + vi) * kHeadDim + 8 * dg, mine);
+      const uint16_t* nw = is_k ? a.kn_w : a.qn_w;
+      norm_rope16(mine, *(const uint4*)(nw + 8 * dg), *(const uint4*)(nw + 64 + 8 * dg), c, sn, a.qk_eps);
+#pragma unroll
+      for (int v = round * 8; v < min(round * 8 + 8, G + 1); ++v) {
+        const int src = (v - round * 8) * 8 + dg;  // lane holding vector v's dims for this dg
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t x = (uint32_t)__shfl((int)mine[e], src);
+          if (v < G) qv[v][e] = x; else kn[e] = x;
+        }
+      }
+    }
   }
   float m[G], l[G], acc[G][16];
 #pragma unroll

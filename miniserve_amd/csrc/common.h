@@ -35,8 +35,24 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
   return __builtin_bit_cast(uint16_t, b);
 }
 __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x8_t __attribute__((ext_vector_type(8)));
+// Two floats -> a bf16 pair (round to nearest even) in one v_cvt_pk_bf16_f32; converting the
+// elements one by one costs a conversion each plus the instructions that pack them.
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+  const f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+
+// Eight int8 weights (bytes of lo, then hi, little-endian) dequantized to bf16(q * s) -- the value
+// of the reference's whole-matrix dequantization (quant/int8.py:36): a sign-extending byte
+// conversion, one multiply and half a packed conversion per weight.
+__device__ __forceinline__ bf16x8 dequant8(uint32_t lo, uint32_t hi, float s) {
+  const f32x8_t f = {(float)(signed char)(lo) * s,       (float)(signed char)(lo >> 8) * s,
+                     (float)(signed char)(lo >> 16) * s, (float)(signed char)(lo >> 24) * s,
+                     (float)(signed char)(hi) * s,       (float)(signed char)(hi >> 8) * s,
+                     (float)(signed char)(hi >> 16) * s, (float)(signed char)(hi >> 24) * s};
+  return __builtin_convertvector(f, bf16x8);
 }
 
 // DPP row (16-lane) all-reduce. Controls: quad_perm [1,0,3,2] = 0xB1, [2,3,0,1] = 0x4E,

@@ -41,18 +41,6 @@ struct GemmArgs {
 
 constexpr int kEpiPartial = 3;  // split-K: store the float32 accumulators, no rounding
 
-__device__ __forceinline__ bf16x8 gemm_dequant8(uint32_t lo, uint32_t hi, float s) {
-  bf16x8 r;
-  r[0] = (__bf16)((float)(signed char)(lo) * s);
-  r[1] = (__bf16)((float)(signed char)(lo >> 8) * s);
-  r[2] = (__bf16)((float)(signed char)(lo >> 16) * s);
-  r[3] = (__bf16)((float)(signed char)(lo >> 24) * s);
-  r[4] = (__bf16)((float)(signed char)(hi) * s);
-  r[5] = (__bf16)((float)(signed char)(hi >> 8) * s);
-  r[6] = (__bf16)((float)(signed char)(hi >> 16) * s);
-  r[7] = (__bf16)((float)(signed char)(hi >> 24) * s);
-  return r;
-}
 
 // Weight row held in LDS row r (0..127) of row block nb.
 template <int EPI>
@@ -117,10 +105,10 @@ __global__ __launch_bounds__(256) void int8_gemm_kernel(GemmArgs a) {
     *(uint4*)(A_ + 64 * kGLd) = ra2;                                                  \
     *(uint4*)(A_ + 96 * kGLd) = ra3;                                                  \
     uint16_t* B_ = Bs + (buf) * kGBN * kGLd + br * kGLd + bc;                         \
-    *(bf16x8*)(B_) = gemm_dequant8(rb0.x, rb0.y, bs[0]);                              \
-    *(bf16x8*)(B_ + 8) = gemm_dequant8(rb0.z, rb0.w, bs[0]);                          \
-    *(bf16x8*)(B_ + 64 * kGLd) = gemm_dequant8(rb1.x, rb1.y, bs[1]);                  \
-    *(bf16x8*)(B_ + 64 * kGLd + 8) = gemm_dequant8(rb1.z, rb1.w, bs[1]);              \
+    *(bf16x8*)(B_) = dequant8(rb0.x, rb0.y, bs[0]);                              \
+    *(bf16x8*)(B_ + 8) = dequant8(rb0.z, rb0.w, bs[0]);                          \
+    *(bf16x8*)(B_ + 64 * kGLd) = dequant8(rb1.x, rb1.y, bs[1]);                  \
+    *(bf16x8*)(B_ + 64 * kGLd + 8) = dequant8(rb1.z, rb1.w, bs[1]);              \
   } while (0)
 
   f32x4 acc[4][4];

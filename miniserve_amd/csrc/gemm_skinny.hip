@@ -43,18 +43,6 @@ struct SkinnyArgs {
   int k_range;     // K handled by one workgroup (multiple of 64)
 };
 
-__device__ __forceinline__ bf16x8 dequant8(uint32_t lo, uint32_t hi, float s) {
-  bf16x8 r;
-  r[0] = (__bf16)((float)(signed char)(lo) * s);
-  r[1] = (__bf16)((float)(signed char)(lo >> 8) * s);
-  r[2] = (__bf16)((float)(signed char)(lo >> 16) * s);
-  r[3] = (__bf16)((float)(signed char)(lo >> 24) * s);
-  r[4] = (__bf16)((float)(signed char)(hi) * s);
-  r[5] = (__bf16)((float)(signed char)(hi >> 8) * s);
-  r[6] = (__bf16)((float)(signed char)(hi >> 16) * s);
-  r[7] = (__bf16)((float)(signed char)(hi >> 24) * s);
-  return r;
-}
 
 __device__ __forceinline__ float silu_mul(float gate_acc, float up_acc) {
   const float g = round_bf16(gate_acc);

@@ -60,23 +60,11 @@ struct DecLinArgs {
   int64_t ldr;
 };
 
-__device__ __forceinline__ bf16x8 dequant8(uint32_t lo, uint32_t hi, float s) {
-  bf16x8 r;
-  r[0] = (__bf16)((float)(signed char)(lo) * s);
-  r[1] = (__bf16)((float)(signed char)(lo >> 8) * s);
-  r[2] = (__bf16)((float)(signed char)(lo >> 16) * s);
-  r[3] = (__bf16)((float)(signed char)(lo >> 24) * s);
-  r[4] = (__bf16)((float)(signed char)(hi) * s);
-  r[5] = (__bf16)((float)(signed char)(hi >> 8) * s);
-  r[6] = (__bf16)((float)(signed char)(hi >> 16) * s);
-  r[7] = (__bf16)((float)(signed char)(hi >> 24) * s);
-  return r;
-}
 
 // bf16(w * bf16(x * r)) on a pair of bf16 (model/layers.py:20-22).
 __device__ __forceinline__ uint32_t norm_pair(uint32_t xv, uint32_t wv, float r) {
-  const float lo = round_bf16(bf16lo(xv) * r), hi = round_bf16(bf16hi(xv) * r);
-  return pack_bf16x2(bf16lo(wv) * lo, bf16hi(wv) * hi);
+  const uint32_t t = pack_bf16x2(bf16lo(xv) * r, bf16hi(xv) * r);  // both bf16(x * r) in one conversion
+  return pack_bf16x2(bf16lo(wv) * bf16lo(t), bf16hi(wv) * bf16hi(t));
 }
 
 // Weight row of tile nt, lane row j. SILU_MUL: tiles [0, NT/2) are gate rows, [NT/2, NT) the
@@ -124,11 +112,11 @@ __global__ __launch_bounds__(64 * KW) __attribute__((amdgpu_waves_per_eu(1, 1)))
   constexpr int XLD = XR * XLPR / 64;  // loads per lane
   static_assert(XLPR == 32, "two rows per load instruction");
   const int xsub = lane >> 5, xcol = (lane & 31) * 8;
-  int64_t gidx = 0;
+  int gidx = 0;  // GATHER: activation row of token tbase + (lane & 31) (rows < 2^31: checked on the host)
   if constexpr (GATHER) {
     const int tl = min(tbase + (lane & 31), a.t - 1);
     const int64_t r = a.gather[tl];
-    gidx = r < 0 ? 0 : (r >= a.x_rows ? a.x_rows - 1 : r);  // memory safety only
+    gidx = (int)(r < 0 ? 0 : (r >= a.x_rows ? a.x_rows - 1 : r));  // memory safety only
   }
   const int8_t* wp[NT];
   uint32_t scb[NT];
@@ -164,13 +152,13 @@ __global__ __launch_bounds__(64 * KW) __attribute__((amdgpu_waves_per_eu(1, 1)))
 #pragma unroll
   for (int i = 0; i < XLD; ++i) {
     const int r = 2 * i + xsub;  // token row within the workgroup's tiles
-    int64_t src_row;
+    int src_row;
     if constexpr (GATHER) {
       src_row = __shfl(gidx, r);
     } else {
       src_row = min(tbase + r, a.t - 1);
     }
-    xr[i] = *(const uint4*)(a.x + src_row * a.ldx + ks * CH * 64 + xcol);
+    xr[i] = *(const uint4*)(a.x + (int64_t)src_row * a.ldx + ks * CH * 64 + xcol);
   }
   uint4 nw[NORM ? CH : 1][2];
   if constexpr (NORM) {
@@ -190,20 +178,21 @@ __global__ __launch_bounds__(64 * KW) __attribute__((amdgpu_waves_per_eu(1, 1)))
   uint16_t* xs = (uint16_t*)s_red + ks * (XR * XP);
 #pragma unroll
   for (int i = 0; i < XLD; ++i) *(uint4*)(xs + (2 * i + xsub) * XP + xcol) = xr[i];
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   if constexpr (GATHER) {
     // The gathered rows are the residual stream's first value (model/qwen3.py:148): one
-    // workgroup per token chunk copies them out, before the norm.
+    // workgroup per token chunk copies them out (from LDS), before the norm.
     if (a.x_copy != nullptr && rb == 0) {
 #pragma unroll
       for (int i = 0; i < XLD; ++i) {
         const int tl = tbase + 2 * i + xsub;
-        if (tl < a.t) *(uint4*)(a.x_copy + (int64_t)tl * a.ld_copy + ks * CH * 64 + xcol) = xr[i];
+        const uint4 v = *(const uint4*)(xs + (2 * i + xsub) * XP + xcol);
+        if (tl < a.t) *(uint4*)(a.x_copy + (int64_t)tl * a.ld_copy + ks * CH * 64 + xcol) = v;
       }
     }
   }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   uint4 xa[MT][CH][2];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
@@ -365,15 +354,19 @@ static int dec_launch(const DecLinArgs& a, hipStream_t s) {
   return MSA_OK;
 }
 
+// Only the shapes dec_shape picks are instantiated: two token tiles or four weight tiles per
+// workgroup only with 4 or 8 wavefronts (more would not fit the register budget).
 template <int NT, int MT, int PRO, int EPI>
 static int dec_dispatch_kw(int kw, const DecLinArgs& a, hipStream_t s) {
+  constexpr bool kWide = MT > 1 || NT > 2;
   switch (kw) {
     case 4: return dec_launch<NT, MT, 4, PRO, EPI>(a, s);
     case 8: return dec_launch<NT, MT, 8, PRO, EPI>(a, s);
-    case 12: return dec_launch<NT, MT, 12, PRO, EPI>(a, s);
-    case 16: return dec_launch<NT, MT, 16, PRO, EPI>(a, s);
-    default: return fail(MSA_ERR_UNSUPPORTED, "decode linear: unsupported in_features");
+    case 12: if constexpr (!kWide) return dec_launch<NT, MT, 12, PRO, EPI>(a, s); break;
+    case 16: if constexpr (!kWide) return dec_launch<NT, MT, 16, PRO, EPI>(a, s); break;
+    default: break;
   }
+  return fail(MSA_ERR_UNSUPPORTED, "decode linear: unsupported in_features / tile shape");
 }
 
 template <int PRO, int EPI>
@@ -449,7 +442,8 @@ extern "C" int msa_int8_linear_dec(const uint16_t* x, int64_t ldx, int64_t x_row
   if (gather_rows && !norm_w) return fail(MSA_ERR_UNSUPPORTED, "msa_int8_linear_dec: gather_rows needs norm_w");
   if (gather_rows && epilogue != MSA_EPI_NONE)
     return fail(MSA_ERR_UNSUPPORTED, "msa_int8_linear_dec: gather_rows takes MSA_EPI_NONE");
-  if (x_rows < (gather_rows ? 1 : m)) return fail(MSA_ERR_INVALID, "msa_int8_linear_dec: x has too few rows");
+  if (x_rows < (gather_rows ? 1 : m) || x_rows > 0x7fffffff)
+    return fail(MSA_ERR_INVALID, "msa_int8_linear_dec: x must have between 1 (m without gather_rows) and 2^31 - 1 rows");
   if (x_copy && (!gather_rows || !aligned16(x_copy) || ld_copy < k || ld_copy % 8 != 0))
     return fail(MSA_ERR_INVALID, "msa_int8_linear_dec: x_copy needs gather_rows, 16-byte alignment and ld_copy >= k");
   if (epilogue == MSA_EPI_SILU_MUL && n % 2 != 0)

@@ -84,18 +84,6 @@ struct RowsArgs {
   int32_t* cand_idx;
 };
 
-__device__ __forceinline__ bf16x8 dequant8_rows(uint32_t lo, uint32_t hi, float s) {
-  bf16x8 r;
-  r[0] = (__bf16)((float)(signed char)(lo) * s);
-  r[1] = (__bf16)((float)(signed char)(lo >> 8) * s);
-  r[2] = (__bf16)((float)(signed char)(lo >> 16) * s);
-  r[3] = (__bf16)((float)(signed char)(lo >> 24) * s);
-  r[4] = (__bf16)((float)(signed char)(hi) * s);
-  r[5] = (__bf16)((float)(signed char)(hi >> 8) * s);
-  r[6] = (__bf16)((float)(signed char)(hi >> 16) * s);
-  r[7] = (__bf16)((float)(signed char)(hi >> 24) * s);
-  return r;
-}
 
 __device__ __forceinline__ float silu_mul_rows(float gate_acc, float up_acc) {
   const float g = round_bf16(gate_acc);
@@ -418,8 +406,8 @@ __global__ __launch_bounds__(64 * RT * KW) void int8_rows_kernel(RowsArgs a) {
             av[mt] = *(const bf16x8*)(xrow + mt * 16 * ldsx + (c0 + c) * kRowsChunk + h * 8);
 #pragma unroll
           for (int nt = 0; nt < NTW; ++nt) {
-            const bf16x8 bv = h == 0 ? dequant8_rows(wv[c][nt].x, wv[c][nt].y, sc[nt])
-                                     : dequant8_rows(wv[c][nt].z, wv[c][nt].w, sc[nt]);
+            const bf16x8 bv = h == 0 ? dequant8(wv[c][nt].x, wv[c][nt].y, sc[nt])
+                                     : dequant8(wv[c][nt].z, wv[c][nt].w, sc[nt]);
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt)
               acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[mt], bv, acc[mt][nt], 0, 0, 0);
