@@ -560,7 +560,12 @@ def kernel_only(mode: str, seed: int) -> int:
                   ("qkv [4096x1024] + q/k-norm/RoPE/cache, 64 tokens", 64, 4096, 1024, -1),
                   ("o [1024x2048] + residual, 64 tokens", 64, 1024, 2048, kernels.EPI_RESIDUAL),
                   ("gate_up [6144x1024] + norm + silu*up, 64 tokens", 64, 6144, 1024, kernels.EPI_SILU_MUL),
-                  ("down [1024x3072] + residual, 64 tokens", 64, 1024, 3072, kernels.EPI_RESIDUAL)]
+                  ("down [1024x3072] + residual, 64 tokens", 64, 1024, 3072, kernels.EPI_RESIDUAL),
+                  # Qwen3-8B-shaped decode linears: weights large enough for a launch to stream at HBM rates
+                  ("8B qkv [6144x4096], 16 tokens", 16, 6144, 4096, kernels.EPI_NONE),
+                  ("8B o [4096x4096] + residual, 16 tokens", 16, 4096, 4096, kernels.EPI_RESIDUAL),
+                  ("8B gate_up [24576x4096] + norm + silu*up, 16 tokens", 16, 24576, 4096, kernels.EPI_SILU_MUL),
+                  ("8B gate_up [24576x4096] + norm + silu*up, 64 tokens", 64, 24576, 4096, kernels.EPI_SILU_MUL)]
         for name, m, n, k, epi in shapes:
             copies = max(8, -(-(300 << 20) // (n * k)))
             ws = torch.randint(-127, 128, (copies, n, k), dtype=torch.int8, device=dev, generator=g)
@@ -600,10 +605,11 @@ def kernel_only(mode: str, seed: int) -> int:
             else:
                 def run_dec(i):
                     kernels.int8_linear_dec(x, ws[i], sc[i], out=y)
+            runs = [("token-split rows kernel", run), ("decode kernel", run_dec)]
             nbytes = linear_bytes(m, n, k)
-            for kind, fn in (("token-split rows kernel", run), ("decode kernel", run_dec)):
+            for kind, fn in runs:
                 secs = hip_time(fn, copies)
-                label = name if not (epi == -1 and kind == "decode kernel") else "qkv [4096x1024] + input norm, 64 tokens"
+                label = name if not (epi == -1 and kind != "token-split rows kernel") else "qkv [4096x1024] + input norm, 64 tokens"
                 print(json.dumps({"linear": label, "kernel": kind, "us_per_launch": round(secs * 1e6, 3),
                                   "bytes_per_launch": nbytes, "GB_s": round(nbytes / secs / 1e9, 1),
                                   "copies": copies}), flush=True)

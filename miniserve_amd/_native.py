@@ -16,7 +16,7 @@ from pathlib import Path
 import torch  # noqa: F401  -- must be imported before the HIP library is loaded
 
 LIB_PATH = Path(__file__).resolve().parent / "libminiserve_amd.so"
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 # name -> (restype, argtypes); mirrors include/miniserve_amd.h.
 SIGNATURES: dict[str, tuple[object, list[object]]] = {

@@ -66,7 +66,9 @@ __device__ __forceinline__ void unpack8(const uint4& v, float (&f)[8]) {
 __device__ __forceinline__ int decode_context(const DecodeArgs& a, int seq) {
   const int ctx = a.ctx[seq];
   const int cap = a.max_blocks * kBlock;
-  return ctx < cap ? ctx : cap;
+  // the same in every lane; saying so keeps the block loop's control flow scalar (a loop the
+  // compiler takes as divergent gets conservative waits on its loads)
+  return __builtin_amdgcn_readfirstlane(ctx < cap ? ctx : cap);
 }
 
 // Workgroup = W wavefronts for one (sequence, KV head, split). Wave w takes blocks b0 + w,
@@ -149,17 +151,22 @@ __global__ __launch_bounds__(64 * W) void paged_decode_kernel(DecodeArgs a) {
   __shared__ float s_ml[W][G][2];
   const int kvh = blockIdx.x, split = blockIdx.y, seq = blockIdx.z;
   const int start = split * a.part_tokens;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar control flow
   const int rp = lane >> 3, dg = lane & 7;
   const int32_t* btr = a.bt + (int64_t)seq * a.max_blocks;
   const int64_t tok_stride = (int64_t)a.kv_heads * kHeadDim;
   const int64_t lane_off = (int64_t)(2 * rp) * tok_stride + (int64_t)kvh * kHeadDim + 8 * dg;
-  // Table entries of this wavefront's first two blocks are read with the context length, not after
-  // it: every index below max_blocks lies inside the table row, and a block past the context
-  // (a padding entry) is loaded but never used.
+  // Lane i holds the table entry of this wavefront's i-th block, bfirst + i * W (a split has at
+  // most 64 blocks per wavefront, checked on the host), read with the context length, not after
+  // it: indices are clamped into the table row, and a block past the context (a padding entry) is
+  // loaded but never used. The block loop then reads entries with readlane and issues no table
+  // loads of its own. Every load below is issued unconditionally -- indices are clamped and dead
+  // loads masked to one address instead of branched around -- so that the compiler's in-order
+  // load counter stays exact and waiting for one block never waits for the next one's loads.
   const int bfirst = start / kBlock + wave;
-  const int ph0 = bfirst < a.max_blocks ? btr[bfirst] : 0;
-  const int ph1 = bfirst + W < a.max_blocks ? btr[bfirst + W] : 0;
+  const int tab = btr[min(bfirst + lane * W, a.max_blocks - 1)];
+  const int ph0 = __builtin_amdgcn_readlane(tab, 0);
   const int64_t qrow = a.qrows[seq];
   const int ctx = decode_context(a, seq);
 
@@ -171,6 +178,22 @@ __global__ __launch_bounds__(64 * W) void paged_decode_kernel(DecodeArgs a) {
     v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w;
     v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
   };
+  // [row rr][half]: rows 2rp + rr, dims 8dg.. (half 0) and 64 + 8dg.. (half 1) of physical block
+  // phys. A dead load (live false) reads the cache's first 16 bytes at every lane: one cache line.
+  auto load_block = [&](int phys, bool live, uint4 (&kr)[2][2], uint4 (&vr)[2][2]) {
+    phys = ((uint32_t)phys < (uint64_t)a.num_blocks) ? phys : 0;  // out-of-range table entries read block 0
+    const int64_t mask = -(int64_t)live;
+    const int64_t base = ((int64_t)phys * kBlock * tok_stride + lane_off) & mask;
+    const int64_t rs = tok_stride & mask, hs = 64 & mask;
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr)
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        kr[rr][hf] = *(const uint4*)(a.kc + base + rr * rs + hf * hs);
+        vr[rr][hf] = *(const uint4*)(a.vc + base + rr * rs + hf * hs);
+      }
+  };
+  uint4 ka[2][2], va[2][2], kb[2][2], vb[2][2];
   const uint16_t* qrow_p = a.q + qrow * a.ldq;
   if constexpr (!QKV) {
 #pragma unroll
@@ -222,21 +245,7 @@ __global__ __launch_bounds__(64 * W) void paged_decode_kernel(DecodeArgs a) {
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[h][e] = 0.f;
   }
-
-  // [row rr][half]: rows 2rp + rr, dims 8dg.. (half 0) and 64 + 8dg.. (half 1) of physical block phys
-  auto load_block = [&](int phys, uint4 (&kr)[2][2], uint4 (&vr)[2][2]) {
-    phys = ((uint32_t)phys < (uint64_t)a.num_blocks) ? phys : 0;  // out-of-range table entries read block 0
-    const int64_t base = (int64_t)phys * kBlock * tok_stride + lane_off;
-#pragma unroll
-    for (int rr = 0; rr < 2; ++rr)
-#pragma unroll
-      for (int hf = 0; hf < 2; ++hf) {
-        kr[rr][hf] = *(const uint4*)(a.kc + base + rr * tok_stride + 64 * hf);
-        vr[rr][hf] = *(const uint4*)(a.vc + base + rr * tok_stride + 64 * hf);
-      }
-  };
-  uint4 ka[2][2], va[2][2], kb[2][2], vb[2][2];
-  if (bfirst < a.max_blocks) load_block(ph0, ka, va);  // before the context length is known
+  load_block(ph0, bfirst < a.max_blocks, ka, va);  // before the context length is checked
   if (start >= ctx) return;  // the reduce kernel merges only splits that hold keys
   // Fused: the cache is read for the keys before the new token, which comes from registers.
   const int end = min(QKV ? ctx - 1 : ctx, start + a.part_tokens);
@@ -271,7 +280,9 @@ __global__ __launch_bounds__(64 * W) void paged_decode_kernel(DecodeArgs a) {
     uint32_t pp[G];
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-      const float bm = rowpair_max(fmaxf(sc[h][0], sc[h][1]));  // finite: row 0 of the block is visible
+      // the block's max over its rows, the same in every lane (finite: row 0 of the block is visible)
+      const float bm = __builtin_bit_cast(
+          float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, rowpair_max(fmaxf(sc[h][0], sc[h][1])))));
       if (bm > m[h]) {  // wave-uniform
         const float alpha = exp2f(m[h] - bm);
         m[h] = bm;
@@ -298,23 +309,20 @@ __global__ __launch_bounds__(64 * W) void paged_decode_kernel(DecodeArgs a) {
     }
   };
 
-  // Two register buffers in turn: the next block's loads are in flight while one is processed,
-  // and the table entry of the block after it is read one step ahead.
-  int b = bfirst;
-  int ph_next = ph1;  // table entry of block b + W
-  while (b < b1) {
-    const int ph_a = b + 2 * W < a.max_blocks ? btr[b + 2 * W] : 0;
-    if (b + W < b1) load_block(ph_next, kb, vb);
-    process(b, ka, va);
-    b += W;
-    ph_next = ph_a;
-    if (b >= b1) break;
-    const int ph_b = b + 2 * W < a.max_blocks ? btr[b + 2 * W] : 0;
-    if (b + W < b1) load_block(ph_next, ka, va);
-    process(b, kb, vb);
-    b += W;
-    ph_next = ph_b;
+  // Two register buffers in turn, the next block's loads in flight while one is processed: pairs
+  // of blocks per iteration and the odd last block after the loop -- a loop with a single exit, so
+  // the compiler's wait counting sees every buffer consumed before it is reloaded. Entry j of the
+  // table (this wavefront's block bfirst + j * W) is lane j of tab.
+  const int nb = bfirst < b1 ? (b1 - bfirst + W - 1) / W : 0;  // this wavefront's blocks
+  auto entry = [&](int j) { return __builtin_amdgcn_readlane(tab, min(j, 63)); };
+  int i = 0;  // block i (ka) is loaded at the top of each iteration
+  for (; i + 2 <= nb; i += 2) {
+    load_block(entry(i + 1), true, kb, vb);
+    process(bfirst + i * W, ka, va);
+    load_block(entry(i + 2), i + 2 < nb, ka, va);
+    process(bfirst + (i + 1) * W, kb, vb);
   }
+  if (i < nb) process(bfirst + i * W, ka, va);
   if constexpr (QKV) {
     // The new token: wavefront 0 of the split holding position ctx - 1 attends to it (row 0 of
     // its lanes' first row pair only) and writes its key and value into the cache.
@@ -622,12 +630,16 @@ extern "C" size_t msa_paged_attention_decode_workspace_size(int num_seqs, int he
 }
 
 namespace msa {
+constexpr int kDecodeW = 4;  // wavefronts per decode workgroup
+// Keys per workgroup-level split: at most 64 blocks per wavefront (one table entry per lane).
+constexpr int kDecodeMaxPartTokens = 64 * kDecodeW * kBlock;
+
 template <int G, bool QKV = false>
 static void launch_decode(const DecodeArgs& a, int num_seqs, hipStream_t s) {
   // Four wavefronts per workgroup: at the kernel's register count (three wavefronts per SIMD for
   // G <= 2) three workgroups share a CU, so a batch's (sequence, KV head) pairs are resident at
   // once.
-  constexpr int W = 4;
+  constexpr int W = kDecodeW;
   const dim3 grid(a.kv_heads, a.splits, num_seqs);
   hipLaunchKernelGGL((paged_decode_kernel<G, W, QKV>), grid, dim3(64 * W), 0, s, a);
 }
@@ -647,6 +659,8 @@ static int decode_args(const char* who, const uint16_t* q, int64_t ldq, const ui
     return fail(MSA_ERR_INVALID, w + ": bad shape (num_seqs <= 65535)");
   if (partition_tokens <= 0 || partition_tokens % kBlock != 0 || max_partitions <= 0 || max_partitions > 65535)
     return fail(MSA_ERR_INVALID, w + ": partition_tokens must be a positive multiple of 16");
+  if (partition_tokens > kDecodeMaxPartTokens)
+    return fail(MSA_ERR_INVALID, w + ": partition_tokens must be at most 4096");
   if ((int64_t)partition_tokens * max_partitions < (int64_t)max_blocks * kBlock)
     return fail(MSA_ERR_INVALID, w + ": partition_tokens * max_partitions must cover max_blocks * 16");
   if (ldq % 8 != 0 || !aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out))

@@ -282,12 +282,17 @@ def reshape_and_cache(k: Tensor, v: Tensor, k_cache: Tensor, v_cache: Tensor, sl
 # ---- paged attention ------------------------------------------------------------------------------
 
 
+DECODE_MAX_PART_BLOCKS = 256  # 16-token blocks per decode split (64 per wavefront)
+
+
 def decode_splits(num_seqs: int, kv_heads: int, max_blocks: int) -> tuple[int, int]:
     """(partition_tokens, partitions) for the decode kernel: one workgroup of four wavefronts per
     (sequence, KV head) when that gives 256+ workgroups; otherwise split each sequence's keys
-    across workgroups (at least four 16-token blocks, one per wavefront, in each)."""
+    across workgroups (at least four 16-token blocks, one per wavefront, in each). A split holds
+    at most 256 blocks (4096 keys)."""
     wgs = max(1, num_seqs * kv_heads)
     splits = 1 if wgs >= 256 else min(-(-512 // wgs), max(1, max_blocks // 4))
+    splits = max(splits, -(-max_blocks // DECODE_MAX_PART_BLOCKS))
     per_blocks = -(-max_blocks // splits)
     return per_blocks * 16, -(-max_blocks // per_blocks)
 

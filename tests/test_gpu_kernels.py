@@ -257,6 +257,18 @@ def test_decode_attention_config2_shape():
         assert rel_l2(out[i], ref[i]) < 1e-2
 
 
+def test_decode_attention_long_contexts_split():
+    """Contexts past one split's 4096 keys in a batch large enough (32 x 8 workgroups) that short
+    contexts alone would take no split: the host splits every sequence's keys in 4096-key pieces."""
+    rng = random.Random(5)
+    specs = [(rng.randint(0, 300), 1) for _ in range(27)] + [(4094, 1), (4095, 1), (4096, 1), (6000, 1), (8191, 1)]
+    assert kernels.decode_splits(32, 8, 8192 // 16)[1] >= 2
+    out, ref, dense = _run_both(specs, 16, 8, seed=5)
+    for i in range(len(specs)):
+        assert rel_l2(out[i], ref[i]) < 1e-2, i
+    assert rel_l2(out, dense) < 1e-2
+
+
 @pytest.mark.parametrize("heads,kv_heads", [(16, 8), (32, 8), (8, 8)])
 def test_prefill_attention(heads, kv_heads):
     # fresh prompts, a chunk after cached keys, speculative-verify-sized rows, ragged tiles
