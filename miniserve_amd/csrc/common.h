@@ -55,6 +55,16 @@ __device__ __forceinline__ bf16x8 dequant8(uint32_t lo, uint32_t hi, float s) {
   return __builtin_convertvector(f, bf16x8);
 }
 
+// Eight int8 weights (bytes of lo, then hi) as bf16, exactly (|q| <= 127 needs 7 mantissa bits):
+// a sign-extending byte conversion and half a packed conversion per weight.
+__device__ __forceinline__ bf16x8 int8x8_to_bf16(uint32_t lo, uint32_t hi) {
+  const f32x8_t f = {(float)(signed char)(lo),       (float)(signed char)(lo >> 8),
+                     (float)(signed char)(lo >> 16), (float)(signed char)(lo >> 24),
+                     (float)(signed char)(hi),       (float)(signed char)(hi >> 8),
+                     (float)(signed char)(hi >> 16), (float)(signed char)(hi >> 24)};
+  return __builtin_convertvector(f, bf16x8);
+}
+
 // DPP row (16-lane) all-reduce. Controls: quad_perm [1,0,3,2] = 0xB1, [2,3,0,1] = 0x4E,
 // row_half_mirror = 0x141, row_mirror = 0x140. After the four steps every lane of a 16-lane row
 // holds the row's total.

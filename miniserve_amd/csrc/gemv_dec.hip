@@ -61,10 +61,10 @@ struct DecLinArgs {
 };
 
 
-// bf16(w * bf16(x * r)) on a pair of bf16 (model/layers.py:20-22).
-__device__ __forceinline__ uint32_t norm_pair(uint32_t xv, uint32_t wv, float r) {
-  const uint32_t t = pack_bf16x2(bf16lo(xv) * r, bf16hi(xv) * r);  // both bf16(x * r) in one conversion
-  return pack_bf16x2(bf16lo(wv) * bf16lo(t), bf16hi(wv) * bf16hi(t));
+// bf16(x * w) on a pair of bf16: the RMSNorm weight applied to the activations; the row factor
+// rsqrt(mean(x^2) + eps) is applied to the finished dot products.
+__device__ __forceinline__ uint32_t weight_pair(uint32_t xv, uint32_t wv) {
+  return pack_bf16x2(bf16lo(xv) * bf16lo(wv), bf16hi(xv) * bf16hi(wv));
 }
 
 // Weight row of tile nt, lane row j. SILU_MUL: tiles [0, NT/2) are gate rows, [NT/2, NT) the
@@ -224,29 +224,20 @@ __global__ __launch_bounds__(64 * KW) __attribute__((amdgpu_waves_per_eu(1, 1)))
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) s_ss[ks][mt * 16 + j] = ss[mt];
     }
-    __syncthreads();
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      float tot = 0.f;
-#pragma unroll
-      for (int w = 0; w < KW; ++w) tot += s_ss[w][mt * 16 + j];
-      const float r = 1.0f / sqrtf(tot / (float)a.k + a.eps);
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int c = 0; c < CH; ++c)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           uint4& v = xa[mt][c][h];
           const uint4 wn = nw[c][h];
-          v = uint4{norm_pair(v.x, wn.x, r), norm_pair(v.y, wn.y, r), norm_pair(v.z, wn.z, r),
-                    norm_pair(v.w, wn.w, r)};
+          v = uint4{weight_pair(v.x, wn.x), weight_pair(v.y, wn.y), weight_pair(v.z, wn.z), weight_pair(v.w, wn.w)};
         }
-    }
+    __syncthreads();  // the row sums of squares are read by the epilogue
   }
 
-  // ---- 3. dequantize once, MFMA over the MT token tiles ----
-  float sc[NT];
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) sc[nt] = bf16_to_f32(scb[nt]);
+  // ---- 3. int8 weights as exact bf16, MFMA over the MT token tiles (scales applied after) ----
   f32x4 acc[MT][NT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
@@ -258,7 +249,7 @@ __global__ __launch_bounds__(64 * KW) __attribute__((amdgpu_waves_per_eu(1, 1)))
     for (int h = 0; h < 2; ++h)
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
-        const bf16x8 bv = h == 0 ? dequant8(wv[nt][c].x, wv[nt][c].y, sc[nt]) : dequant8(wv[nt][c].z, wv[nt][c].w, sc[nt]);
+        const bf16x8 bv = h == 0 ? int8x8_to_bf16(wv[nt][c].x, wv[nt][c].y) : int8x8_to_bf16(wv[nt][c].z, wv[nt][c].w);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
           acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xa[mt][c][h]), bv,
@@ -294,18 +285,36 @@ __global__ __launch_bounds__(64 * KW) __attribute__((amdgpu_waves_per_eu(1, 1)))
     const int col = SILU ? (rb * NP + np) * 16 + j : dec_row<NT, EPI>(a, rb, np, j);
     const int ncols = SILU ? a.n / 2 : a.n;
     if (col >= ncols) continue;
+    // this lane's column scale(s) (weight row j of tile np / np + NP) and row factors
+    uint32_t sb0 = 0, sb1 = 0;  // selected with constant indices (np varies by wavefront)
+#pragma unroll
+    for (int nt = 0; nt < NP; ++nt) {
+      sb0 = nt == np ? scb[nt] : sb0;
+      if constexpr (SILU) sb1 = nt == np ? scb[nt + NP] : sb1;
+    }
+    const float s0 = bf16_to_f32(sb0), s1 = bf16_to_f32(sb1);
+    float rf[4] = {1.f, 1.f, 1.f, 1.f};
+    if constexpr (NORM) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float tot = 0.f;
+#pragma unroll
+        for (int w = 0; w < KW; ++w) tot += s_ss[w][mt * 16 + 4 * g + i];
+        rf[i] = 1.0f / sqrtf(tot / (float)a.k + a.eps);
+      }
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int tl = tbase + mt * 16 + 4 * g + i;
       if (tl >= a.t) continue;
       float o;
       if constexpr (SILU) {
-        const float gt = round_bf16(v0[i]), up = round_bf16(v1[i]);
+        const float gt = round_bf16(v0[i] * (rf[i] * s0)), up = round_bf16(v1[i] * (rf[i] * s1));
         o = round_bf16(gt / (1.0f + expf(-gt))) * up;
       } else if constexpr (EPI == DL_EPI_RESIDUAL) {
-        o = round_bf16(v0[i]) + bf16_to_f32(rres[uu][i]);
+        o = round_bf16(v0[i] * (rf[i] * s0)) + bf16_to_f32(rres[uu][i]);
       } else {
-        o = v0[i];
+        o = v0[i] * (rf[i] * s0);
       }
       a.y[(int64_t)tl * a.ldy + col] = f32_to_bf16(o);
     }
