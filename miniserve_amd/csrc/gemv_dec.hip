@@ -11,16 +11,20 @@
 //     (the A operand of v_mfma_f32_16x16x32_bf16: token row j, 16 consecutive K values per chunk),
 //     the norm weights, its int8 weight fragments (B operand: weight row j, 16 bytes per chunk),
 //     the row scales and the residual values its epilogue will add.
-//  2. RMSNorm prologue (model/layers.py:18-22 rounding: bf16(w * bf16(x * rsqrt(mean(x^2) + eps)))):
-//     each wavefront sums the squares of its K slice on bf16 pairs (v_dot2_f32_bf16), the KW
-//     partial sums of each token meet in LDS (one barrier), and each lane normalizes its own
-//     fragments in registers.
-//  3. Each 16-byte weight fragment is dequantized once to bf16(q * s) -- the value the reference's
-//     whole-matrix dequantization produces (quant/int8.py:36) -- and feeds the MT token tiles.
+//  2. RMSNorm prologue (model/layers.py:18-22): each wavefront sums the squares of its K slice on
+//     bf16 pairs (v_dot2_f32_bf16), the KW partial sums of each token meet in LDS (one barrier),
+//     and each lane multiplies its own fragments by the norm weight, bf16(x * w). The row factor
+//     rsqrt(mean(x^2) + eps) is linear in the product and is applied in the epilogue.
+//  3. Each 16-byte weight fragment is converted once to bf16 -- exactly: |q| <= 127 -- and feeds
+//     the MT token tiles. The per-row scale (quant/int8.py:36) is likewise applied in the epilogue,
+//     to the float32 dot product: y = r * s * sum(x * w * q). The reference instead rounds
+//     bf16(q * s) and bf16(w * bf16(x * r)) element by element before its bf16 product; the two
+//     differ by those roundings (rel-L2 ~4e-3), and this form is the closer of the two to the
+//     float64 value of the same int8 weights (~2e-3 against ~3e-3).
 //  4. The KW partial accumulators meet in LDS (second barrier); the output tiles are spread over
 //     the wavefronts, each summing the KW partials in a fixed order (deterministic) and applying
-//     the epilogue: plain bf16 store, residual add (model/qwen3.py:121-122) or silu(gate) * up with
-//     the gate and up tiles in the same workgroup (model/layers.py:77-78).
+//     r * s and the epilogue: plain bf16 store, residual add (model/qwen3.py:121-122) or
+//     silu(gate) * up with the gate and up tiles in the same workgroup (model/layers.py:77-78).
 //
 // The K mapping inside a 64-wide chunk is permuted identically for A and B (lane group g takes K
 // offsets [16g, 16g + 16) and splits them over the two MFMA k-steps), which leaves the dot
