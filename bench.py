@@ -45,7 +45,7 @@ BATCH, CTX_LO, CTX_HI = 64, 256, 384
 # FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 of one fused decode-attention launch on the decode workload,
 # from rocprofv3 --pmc: 42,902.07 KiB x 2 x 1024 + 512 KiB x 1024
 # (profiles/paged_decode_kernel_traffic_pmc.md).
-ATTN_TRAFFIC_BYTES: int | None = 88_387_737
+ATTN_TRAFFIC_BYTES: int | None = 88_321_135
 
 
 def log(msg: str) -> None:
