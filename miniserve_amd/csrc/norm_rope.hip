@@ -165,6 +165,111 @@ __global__ __launch_bounds__(256) void qk_norm_rope_cache_kernel(
   }
 }
 
+// The same op for head_dim 128 with 16-byte accesses: one workgroup per (token, 32 head slots),
+// eight threads per head slot. Thread (slot, sub) holds dims [8 sub, 8 sub + 8) and their RoPE
+// partners [64 + 8 sub, 64 + 8 sub + 8), so every rotation pair is in one thread; the head's sum of
+// squares meets over the eight threads. All loads of a thread are issued before any use: one
+// memory round trip per token instead of one per dependent step.
+template <bool PARTIAL>
+__global__ __launch_bounds__(256) void qk_norm_rope_cache_d128_kernel(
+    const uint16_t* __restrict__ qkv, int64_t ldqkv, const float* __restrict__ part, int k_split, int64_t tokens,
+    int heads, int kv_heads, const uint16_t* __restrict__ qw, const uint16_t* __restrict__ kw, float eps,
+    const float* __restrict__ cos_t, const float* __restrict__ sin_t, const int64_t* __restrict__ slots,
+    uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache, int64_t num_slots) {
+  constexpr int D = 128;
+  const int nslots = heads + 2 * kv_heads;
+  const int groups = (nslots + 31) / 32;
+  const int64_t t = blockIdx.x / groups;
+  const int hs = (int)(blockIdx.x % groups) * 32 + (int)(threadIdx.x >> 3);
+  const int sub = threadIdx.x & 7;
+  const bool live = hs < nslots;
+  const int hsc = live ? hs : nslots - 1;  // idle threads read a real slot and store nothing
+  const int d0 = 8 * sub, d1 = 64 + 8 * sub;
+  // the head slot's 16 values, as floats (bf16-rounded partial sums for PARTIAL)
+  float lo[8], hi[8];
+  if constexpr (PARTIAL) {
+    const int64_t row_cols = (int64_t)nslots * D, pstride = tokens * row_cols;
+    const float* p = part + t * row_cols + (int64_t)hsc * D;
+    float4 a0 = *(const float4*)(p + d0), a1 = *(const float4*)(p + d0 + 4);
+    float4 b0 = *(const float4*)(p + d1), b1 = *(const float4*)(p + d1 + 4);
+    for (int s = 1; s < k_split; ++s) {
+      const float* q = p + s * pstride;
+      const float4 c0 = *(const float4*)(q + d0), c1 = *(const float4*)(q + d0 + 4);
+      const float4 e0 = *(const float4*)(q + d1), e1 = *(const float4*)(q + d1 + 4);
+      a0.x += c0.x; a0.y += c0.y; a0.z += c0.z; a0.w += c0.w; a1.x += c1.x; a1.y += c1.y; a1.z += c1.z; a1.w += c1.w;
+      b0.x += e0.x; b0.y += e0.y; b0.z += e0.z; b0.w += e0.w; b1.x += e1.x; b1.y += e1.y; b1.z += e1.z; b1.w += e1.w;
+    }
+    const float la[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    const float lb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      lo[e] = round_bf16(la[e]);
+      hi[e] = round_bf16(lb[e]);
+    }
+  } else {
+    const uint16_t* src = qkv + t * ldqkv + (int64_t)hsc * D;
+    const uint4 ul = *(const uint4*)(src + d0), uh = *(const uint4*)(src + d1);
+    const uint32_t wl[4] = {ul.x, ul.y, ul.z, ul.w}, wh[4] = {uh.x, uh.y, uh.z, uh.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      lo[2 * e] = bf16lo(wl[e]);
+      lo[2 * e + 1] = bf16hi(wl[e]);
+      hi[2 * e] = bf16lo(wh[e]);
+      hi[2 * e + 1] = bf16hi(wh[e]);
+    }
+  }
+  const bool is_q = hsc < heads, is_v = hsc >= heads + kv_heads;
+  const uint16_t* nw = is_q ? qw : kw;
+  const uint4 nl = *(const uint4*)(nw + d0), nh = *(const uint4*)(nw + d1);
+  const float* cr = cos_t + t * D;
+  const float* sr = sin_t + t * D;
+  const float4 cl0 = *(const float4*)(cr + d0), cl1 = *(const float4*)(cr + d0 + 4);
+  const float4 ch0 = *(const float4*)(cr + d1), ch1 = *(const float4*)(cr + d1 + 4);
+  const float4 sl0 = *(const float4*)(sr + d0), sl1 = *(const float4*)(sr + d0 + 4);
+  const float4 sh0 = *(const float4*)(sr + d1), sh1 = *(const float4*)(sr + d1 + 4);
+  const int64_t slot = slots[t];
+  const bool cached = slot >= 0 && slot < num_slots;
+
+  if (is_v) {
+    if (live && cached) {
+      uint16_t* dst = v_cache + (slot * kv_heads + (hsc - heads - kv_heads)) * D;
+      *(uint4*)(dst + d0) = uint4{pack_bf16x2(lo[0], lo[1]), pack_bf16x2(lo[2], lo[3]), pack_bf16x2(lo[4], lo[5]),
+                                  pack_bf16x2(lo[6], lo[7])};
+      *(uint4*)(dst + d1) = uint4{pack_bf16x2(hi[0], hi[1]), pack_bf16x2(hi[2], hi[3]), pack_bf16x2(hi[4], hi[5]),
+                                  pack_bf16x2(hi[6], hi[7])};
+    }
+    return;  // the eight threads of a head slot leave together
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss += lo[e] * lo[e] + hi[e] * hi[e];
+  ss += __shfl_xor(ss, 1);
+  ss += __shfl_xor(ss, 2);
+  ss += __shfl_xor(ss, 4);
+  const float r = 1.0f / sqrtf(ss / (float)D + eps);
+  const uint32_t wl[4] = {nl.x, nl.y, nl.z, nl.w}, wh[4] = {nh.x, nh.y, nh.z, nh.w};
+  const float cl[8] = {cl0.x, cl0.y, cl0.z, cl0.w, cl1.x, cl1.y, cl1.z, cl1.w};
+  const float ch[8] = {ch0.x, ch0.y, ch0.z, ch0.w, ch1.x, ch1.y, ch1.z, ch1.w};
+  const float sl[8] = {sl0.x, sl0.y, sl0.z, sl0.w, sl1.x, sl1.y, sl1.z, sl1.w};
+  const float sh[8] = {sh0.x, sh0.y, sh0.z, sh0.w, sh1.x, sh1.y, sh1.z, sh1.w};
+  float ol[8], oh[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float wlo = (e & 1) ? bf16hi(wl[e >> 1]) : bf16lo(wl[e >> 1]);
+    const float whi = (e & 1) ? bf16hi(wh[e >> 1]) : bf16lo(wh[e >> 1]);
+    const float a = round_bf16(wlo * round_bf16(lo[e] * r));
+    const float b = round_bf16(whi * round_bf16(hi[e] * r));
+    ol[e] = round_bf16(a * round_bf16(cl[e])) + round_bf16(-b * round_bf16(sl[e]));
+    oh[e] = round_bf16(b * round_bf16(ch[e])) + round_bf16(a * round_bf16(sh[e]));
+  }
+  if (!live || (!is_q && !cached)) return;
+  uint16_t* dst = is_q ? q_out + (t * heads + hsc) * D : k_cache + (slot * kv_heads + (hsc - heads)) * D;
+  *(uint4*)(dst + d0) = uint4{pack_bf16x2(ol[0], ol[1]), pack_bf16x2(ol[2], ol[3]), pack_bf16x2(ol[4], ol[5]),
+                              pack_bf16x2(ol[6], ol[7])};
+  *(uint4*)(dst + d1) = uint4{pack_bf16x2(oh[0], oh[1]), pack_bf16x2(oh[2], oh[3]), pack_bf16x2(oh[4], oh[5]),
+                              pack_bf16x2(oh[6], oh[7])};
+}
+
 // Residual add + RMSNorm whose delta arrives as k_split float32 split-K partials [k_split][rows][dim]
 // of the projection before it: delta = bf16(sum of partials in split order), residual_out =
 // bf16(residual + delta), out = RMSNorm(residual_out). One workgroup per row.
@@ -272,6 +377,16 @@ static int qk_common_checks(const char* fn, int64_t tokens, int heads, int kv_he
   return MSA_OK;
 }
 
+// The 16-byte-access kernel's preconditions (else the per-element kernel runs).
+static bool qk_d128_ok(int head_dim, int64_t tokens, int heads, int kv_heads, const void* qw, const void* kw,
+                       const void* cos, const void* sin, const void* q_out, const void* k_cache,
+                       const void* v_cache) {
+  using namespace msa;
+  return head_dim == 128 && tokens * ((heads + 2 * kv_heads + 31) / 32) <= 0x7fffffff && aligned16(qw) &&
+         aligned16(kw) && aligned16(cos) && aligned16(sin) && aligned16(q_out) && aligned16(k_cache) &&
+         aligned16(v_cache);
+}
+
 extern "C" int msa_qk_norm_rope_cache(const uint16_t* qkv, int64_t ldqkv, int64_t tokens, int heads, int kv_heads,
                                       int head_dim, const uint16_t* q_norm_w, const uint16_t* k_norm_w, float eps,
                                       const float* cos, const float* sin, const int64_t* slot_mapping,
@@ -285,6 +400,14 @@ extern "C" int msa_qk_norm_rope_cache(const uint16_t* qkv, int64_t ldqkv, int64_
   if (rc != MSA_OK) return rc;
   if (ldqkv < (int64_t)(heads + 2 * kv_heads) * head_dim)
     return fail(MSA_ERR_INVALID, "msa_qk_norm_rope_cache: ldqkv too small");
+  if (qk_d128_ok(head_dim, tokens, heads, kv_heads, q_norm_w, k_norm_w, cos, sin, q_out, k_cache, v_cache) &&
+      aligned16(qkv) && ldqkv % 8 == 0) {
+    const int64_t blocks = tokens * ((heads + 2 * kv_heads + 31) / 32);
+    hipLaunchKernelGGL(qk_norm_rope_cache_d128_kernel<false>, dim3((unsigned)blocks), dim3(256), 0,
+                       (hipStream_t)stream, qkv, ldqkv, nullptr, 0, tokens, heads, kv_heads, q_norm_w, k_norm_w, eps,
+                       cos, sin, slot_mapping, q_out, k_cache, v_cache, num_slots);
+    return check_launch("msa_qk_norm_rope_cache");
+  }
   const int64_t waves = tokens * (heads + 2 * kv_heads);
   hipLaunchKernelGGL(qk_norm_rope_cache_kernel<false>, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0,
                      (hipStream_t)stream, qkv, ldqkv, nullptr, 0, tokens, heads, kv_heads, head_dim, q_norm_w,
@@ -303,6 +426,14 @@ extern "C" int msa_qk_norm_rope_cache_splitk(const float* partials, int k_split,
   int rc = qk_common_checks("msa_qk_norm_rope_cache_splitk", tokens, heads, kv_heads, head_dim, q_norm_w, k_norm_w,
                             cos, sin, slot_mapping, q_out, k_cache, v_cache);
   if (rc != MSA_OK) return rc;
+  if (qk_d128_ok(head_dim, tokens, heads, kv_heads, q_norm_w, k_norm_w, cos, sin, q_out, k_cache, v_cache) &&
+      aligned16(partials)) {
+    const int64_t blocks = tokens * ((heads + 2 * kv_heads + 31) / 32);
+    hipLaunchKernelGGL(qk_norm_rope_cache_d128_kernel<true>, dim3((unsigned)blocks), dim3(256), 0,
+                       (hipStream_t)stream, nullptr, 0, partials, k_split, tokens, heads, kv_heads, q_norm_w,
+                       k_norm_w, eps, cos, sin, slot_mapping, q_out, k_cache, v_cache, num_slots);
+    return check_launch("msa_qk_norm_rope_cache_splitk");
+  }
   const int64_t waves = tokens * (heads + 2 * kv_heads);
   hipLaunchKernelGGL(qk_norm_rope_cache_kernel<true>, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0,
                      (hipStream_t)stream, nullptr, 0, partials, k_split, tokens, heads, kv_heads, head_dim, q_norm_w,
