@@ -166,6 +166,18 @@ int msa_add_rmsnorm(const uint16_t* residual, const uint16_t* delta, uint16_t* r
 /* msa_add_rmsnorm whose delta is the bf16 sum of k_split float32 partials [k_split][rows][dim]
  * from msa_int8_linear_splitk -- the o_proj / down_proj output, residual add and the following
  * RMSNorm of Qwen3DecoderLayer.forward (model/qwen3.py:121-122) in one kernel. dim % 4 == 0. */
+/* The o / down projection of a layer with the next RMSNorm (model/qwen3.py:121-122 then
+ * model/layers.py:18-22): residual = bf16(residual + bf16(x @ bf16(q * s)^T)) in place, then
+ * out = RMSNorm(residual) with norm_w, eps. x [m, k] (row stride ldx), qweight [n, k], residual and
+ * out [m, n] contiguous, n % 8 == 0, 16-byte aligned. When the GEMM splits K (128+ rows, few
+ * output tiles) the float32 partials go to workspace (msa_int8_linear_workspace_size bytes) and
+ * one kernel merges them, adds the residual and normalizes -- the split-K merge and the norm
+ * launch of the unfused sequence become one pass. */
+int msa_int8_linear_add_rmsnorm(const uint16_t* x, int64_t m, int64_t k, int64_t ldx, const int8_t* qweight,
+                                const uint16_t* scale, int64_t n, uint16_t* residual, const uint16_t* norm_w,
+                                float eps, uint16_t* out, void* workspace, size_t workspace_bytes,
+                                msa_stream_t stream);
+
 int msa_splitk_add_rmsnorm(const float* partials, int k_split, const uint16_t* residual,
                            uint16_t* residual_out, const uint16_t* weight, uint16_t* out, int64_t rows,
                            int64_t dim, float eps, msa_stream_t stream);

@@ -16,7 +16,7 @@ from pathlib import Path
 import torch  # noqa: F401  -- must be imported before the HIP library is loaded
 
 LIB_PATH = Path(__file__).resolve().parent / "libminiserve_amd.so"
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 # name -> (restype, argtypes); mirrors include/miniserve_amd.h.
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
@@ -36,6 +36,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "msa_int8_linear_splitk": (
         c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int, c_void_p, c_void_p]
+    ),
+    "msa_int8_linear_add_rmsnorm": (
+        c_int,
+        [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_float, c_void_p,
+         c_void_p, c_size_t, c_void_p],
     ),
     "msa_splitk_add_rmsnorm": (
         c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_float, c_void_p]

@@ -268,6 +268,26 @@ int gemm_run(const uint16_t* x, int64_t m, int64_t k, int64_t ldx, const int8_t*
   return check_launch("msa_int8_gemm");
 }
 
+// The split-K partial pass alone: float32 partials [splits][m][n] of x @ bf16(q * s)^T into part,
+// with the split count the GEMM would use; returns 1 (nothing launched) when it would not split or
+// part is too small.
+int gemm_run_partials(const uint16_t* x, int64_t m, int64_t k, int64_t ldx, const int8_t* qweight,
+                      const uint16_t* scale, int64_t n, float* part, size_t part_bytes, hipStream_t s) {
+  const int splits = gemm_splits(m, n, k, MSA_EPI_NONE);
+  if (splits <= 1 || !part || part_bytes < gemm_workspace_size(m, n, k, MSA_EPI_NONE) || !aligned16(part)) return 1;
+  GemmArgs a{};
+  a.x = x; a.ldx = ldx; a.w = qweight; a.scale = scale;
+  a.m = (int)m; a.n = (int)n; a.k = (int)k;
+  a.n_blocks = (int)((n + kGBN - 1) / kGBN);
+  a.m_blocks = (int)((m + kGBM - 1) / kGBM);
+  a.k_per = (int)(k / splits);
+  a.part = part;
+  const int64_t blocks = (int64_t)a.n_blocks * a.m_blocks * splits;
+  if (blocks > 0x7fffffff) return 1;
+  if (launch_gemm<kEpiPartial>(a, (int)blocks, s) != MSA_OK) return -1;
+  return splits;
+}
+
 // ---- LM head for many rows: gather + RMSNorm once, then a bf16 GEMM with an argmax epilogue ----
 //
 // When the sampled rows do not fit one LDS activation tile of the streaming LM head (many rows at

@@ -269,6 +269,12 @@ int gemm_run(const uint16_t* x, int64_t m, int64_t k, int64_t ldx, const int8_t*
              int64_t n, uint16_t* y, int64_t ldy, int epilogue, const uint16_t* residual, int64_t ldr, void* workspace,
              size_t workspace_bytes, hipStream_t s);
 size_t gemm_workspace_size(int64_t m, int64_t n, int64_t k, int epilogue);
+int gemm_run_partials(const uint16_t* x, int64_t m, int64_t k, int64_t ldx, const int8_t* qweight,
+                      const uint16_t* scale, int64_t n, float* part, size_t part_bytes, hipStream_t s);
+void launch_splitk_add_rmsnorm(const float* part, int k_split, int64_t rows, int dim, const uint16_t* resid_in,
+                               uint16_t* resid_out, const uint16_t* w, uint16_t* out, float eps, hipStream_t s);
+void launch_rmsnorm(const uint16_t* x, int64_t ldx, const uint16_t* w, uint16_t* out, int64_t ldo, int64_t rows, int dim,
+                    float eps, hipStream_t s);
 }  // namespace msa
 
 extern "C" size_t msa_int8_linear_workspace_size(int64_t m, int64_t n, int64_t k) {
@@ -365,4 +371,34 @@ extern "C" int msa_int8_linear_splitk(const uint16_t* x, int64_t m, int64_t k, i
   a.partial = partials; a.k_range = p.k_range;
   launch_skinny<kEpiPartial>(p, a, (hipStream_t)stream);
   return check_launch("msa_int8_linear_splitk");
+}
+
+extern "C" int msa_int8_linear_add_rmsnorm(const uint16_t* x, int64_t m, int64_t k, int64_t ldx,
+                                           const int8_t* qweight, const uint16_t* scale, int64_t n,
+                                           uint16_t* residual, const uint16_t* norm_w, float eps, uint16_t* out,
+                                           void* workspace, size_t workspace_bytes, msa_stream_t stream) {
+  using namespace msa;
+  if (m == 0) return MSA_OK;
+  int rc = check_linear_args("msa_int8_linear_add_rmsnorm", x, m, k, ldx, qweight, scale, n);
+  if (rc != MSA_OK) return rc;
+  if (!residual || !norm_w || !out) return fail(MSA_ERR_INVALID, "msa_int8_linear_add_rmsnorm: null pointer");
+  if (n % 8 != 0 || n > (1 << 20) || !aligned16(residual) || !aligned16(norm_w) || !aligned16(out))
+    return fail(MSA_ERR_UNSUPPORTED,
+                "msa_int8_linear_add_rmsnorm: n must be a multiple of 8 and residual / norm_w / out 16-byte aligned");
+  hipStream_t s = (hipStream_t)stream;
+  if (m >= kGemmMinRows && k % 64 == 0) {
+    const int splits = gemm_run_partials(x, m, k, ldx, qweight, scale, n, (float*)workspace, workspace_bytes, s);
+    if (splits < 0) return MSA_ERR_LAUNCH;
+    if (splits > 1) {
+      rc = check_launch("msa_int8_linear_add_rmsnorm (split-K pass)");
+      if (rc != MSA_OK) return rc;
+      launch_splitk_add_rmsnorm((const float*)workspace, splits, m, (int)n, residual, residual, norm_w, out, eps, s);
+      return check_launch("msa_int8_linear_add_rmsnorm (merge + norm)");
+    }
+  }
+  rc = msa_int8_linear(x, m, k, ldx, qweight, scale, n, residual, n, MSA_EPI_RESIDUAL, residual, n, workspace,
+                       workspace_bytes, stream);
+  if (rc != MSA_OK) return rc;
+  launch_rmsnorm(residual, n, norm_w, out, n, m, (int)n, eps, s);
+  return check_launch("msa_int8_linear_add_rmsnorm (norm)");
 }

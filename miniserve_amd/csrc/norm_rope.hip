@@ -315,6 +315,79 @@ __global__ __launch_bounds__(256) void splitk_add_rmsnorm_kernel(const float* __
   }
 }
 
+// The same for dim = 1024 * NCH (NCH <= 4): every thread keeps its NCH groups of four values in
+// registers between the sum of squares and the normalization, and issues all of its loads
+// (partials, residual, norm weight) before the first use.
+template <int NCH>
+__global__ __launch_bounds__(256) void splitk_add_rmsnorm_reg_kernel(const float* __restrict__ part, int k_split,
+                                                                     int64_t rows, const uint16_t* resid_in,
+                                                                     uint16_t* resid_out, const uint16_t* __restrict__ w,
+                                                                     uint16_t* __restrict__ out, float eps) {
+  constexpr int dim = 1024 * NCH;
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int64_t stride = rows * dim;
+  const float* pr = part + row * dim;
+  float4 acc[NCH];
+  uint2 rv[NCH], wv[NCH];
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    const int c = tid * 4 + i * 1024;
+    acc[i] = *(const float4*)(pr + c);
+    rv[i] = *(const uint2*)(resid_in + row * dim + c);
+    wv[i] = *(const uint2*)(w + c);
+  }
+  for (int s = 1; s < k_split; ++s) {  // split order, as the unfused merge sums them
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const float4 v = *(const float4*)(pr + s * stride + tid * 4 + i * 1024);
+      acc[i].x += v.x; acc[i].y += v.y; acc[i].z += v.z; acc[i].w += v.w;
+    }
+  }
+  float x[NCH][4];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    x[i][0] = round_bf16(round_bf16(acc[i].x) + bf16lo(rv[i].x));
+    x[i][1] = round_bf16(round_bf16(acc[i].y) + bf16hi(rv[i].x));
+    x[i][2] = round_bf16(round_bf16(acc[i].z) + bf16lo(rv[i].y));
+    x[i][3] = round_bf16(round_bf16(acc[i].w) + bf16hi(rv[i].y));
+    ss += x[i][0] * x[i][0] + x[i][1] * x[i][1] + x[i][2] * x[i][2] + x[i][3] * x[i][3];
+    *(uint2*)(resid_out + row * dim + tid * 4 + i * 1024) = uint2{pack_bf16x2(x[i][0], x[i][1]), pack_bf16x2(x[i][2], x[i][3])};
+  }
+  ss = wave_sum(ss);
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
+  __syncthreads();
+  ss = red[0] + red[1] + red[2] + red[3];
+  const float r = 1.0f / sqrtf(ss / (float)dim + eps);
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    const float a0 = round_bf16(x[i][0] * r), a1 = round_bf16(x[i][1] * r);
+    const float a2 = round_bf16(x[i][2] * r), a3 = round_bf16(x[i][3] * r);
+    *(uint2*)(out + row * dim + tid * 4 + i * 1024) =
+        uint2{pack_bf16x2(bf16lo(wv[i].x) * a0, bf16hi(wv[i].x) * a1), pack_bf16x2(bf16lo(wv[i].y) * a2, bf16hi(wv[i].y) * a3)};
+  }
+}
+
+// Host launchers shared with the linear entry points (pointers and shapes checked by the caller).
+void launch_splitk_add_rmsnorm(const float* part, int k_split, int64_t rows, int dim, const uint16_t* resid_in,
+                               uint16_t* resid_out, const uint16_t* w, uint16_t* out, float eps, hipStream_t s) {
+  const dim3 grid((unsigned)rows), block(256);
+  switch (dim) {
+    case 1024: hipLaunchKernelGGL(splitk_add_rmsnorm_reg_kernel<1>, grid, block, 0, s, part, k_split, rows, resid_in, resid_out, w, out, eps); return;
+    case 2048: hipLaunchKernelGGL(splitk_add_rmsnorm_reg_kernel<2>, grid, block, 0, s, part, k_split, rows, resid_in, resid_out, w, out, eps); return;
+    case 4096: hipLaunchKernelGGL(splitk_add_rmsnorm_reg_kernel<4>, grid, block, 0, s, part, k_split, rows, resid_in, resid_out, w, out, eps); return;
+    default: hipLaunchKernelGGL(splitk_add_rmsnorm_kernel, grid, block, 0, s, part, k_split, rows, dim, resid_in, resid_out, w, out, eps);
+  }
+}
+
+void launch_rmsnorm(const uint16_t* x, int64_t ldx, const uint16_t* w, uint16_t* out, int64_t ldo, int64_t rows, int dim,
+                    float eps, hipStream_t s) {
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, x, ldx, w, out, ldo, rows, dim,
+                     eps);
+}
+
 // One thread per 8-element (16-byte) piece of a (token, kv head) row of k and of v.
 __global__ __launch_bounds__(256) void reshape_and_cache_kernel(const uint16_t* __restrict__ k, int64_t ldk,
                                                                 const uint16_t* __restrict__ v, int64_t ldv,
@@ -454,8 +527,8 @@ extern "C" int msa_splitk_add_rmsnorm(const float* partials, int k_split, const 
       (reinterpret_cast<uintptr_t>(residual_out) & 7u) || (reinterpret_cast<uintptr_t>(weight) & 7u) ||
       (reinterpret_cast<uintptr_t>(out) & 7u))
     return fail(MSA_ERR_UNSUPPORTED, "msa_splitk_add_rmsnorm: dim must be a multiple of 4, pointers aligned");
-  hipLaunchKernelGGL(splitk_add_rmsnorm_kernel, dim3((unsigned)rows), dim3(256), 0, (hipStream_t)stream, partials,
-                     k_split, rows, (int)dim, residual, residual_out, weight, out, eps);
+  launch_splitk_add_rmsnorm(partials, k_split, rows, (int)dim, residual, residual_out, weight, out, eps,
+                            (hipStream_t)stream);
   return check_launch("msa_splitk_add_rmsnorm");
 }
 

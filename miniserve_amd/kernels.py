@@ -126,6 +126,34 @@ def int8_linear(
     return out
 
 
+def int8_linear_add_rmsnorm(
+    x: Tensor, qweight: Tensor, scale: Tensor, residual: Tensor, norm_w: Tensor, eps: float, out: Tensor | None = None
+) -> Tensor:
+    """residual += x @ bf16(qweight * scale)^T (bf16 rounding of the product and the sum, in place),
+    then returns RMSNorm(residual) with norm_w: the o / down projection with the next norm
+    (model/qwen3.py:121-122). A GEMM that splits K merges its partials, adds and normalizes in one
+    kernel (msa_int8_linear_add_rmsnorm)."""
+    _on_gpu(x, qweight, scale, residual, norm_w)
+    _check(x.dtype == torch.bfloat16 and x.dim() == 2 and x.stride(-1) == 1, "int8_linear_add_rmsnorm: x [m, k] bf16")
+    _check(qweight.dtype == torch.int8 and qweight.is_contiguous(), "int8_linear_add_rmsnorm: bad qweight")
+    n, k = qweight.shape
+    m = x.shape[0]
+    _check(x.shape[1] == k, "int8_linear_add_rmsnorm: x / weight feature mismatch")
+    _check(residual.shape == (m, n) and residual.is_contiguous() and residual.dtype == torch.bfloat16,
+           "int8_linear_add_rmsnorm: residual [m, n] contiguous bf16")
+    _check(norm_w.dtype == torch.bfloat16 and norm_w.numel() == n, "int8_linear_add_rmsnorm: norm weight")
+    if out is None:
+        out = torch.empty_like(residual)
+    _check(out.shape == (m, n) and out.is_contiguous(), "int8_linear_add_rmsnorm: bad out")
+    ws_bytes = _native.query("msa_int8_linear_workspace_size", m, n, k) if m else 0
+    ws = workspaces.get("linear", x.device, ws_bytes)
+    _native.call(
+        "msa_int8_linear_add_rmsnorm", _ptr(x), m, k, x.stride(0), _ptr(qweight), _ptr(scale), n, _ptr(residual),
+        _ptr(norm_w), float(eps), _ptr(out), _ptr(ws), ws.numel() if ws is not None else 0, _stream(x),
+    )
+    return out
+
+
 def default_split(m: int, n: int, k: int) -> int:
     """K splits for a split-K linear: none when the 32-row x 64-row output tiles give 128+
     workgroups, else about 256 workgroups, each split a whole multiple of four 64-wide K chunks

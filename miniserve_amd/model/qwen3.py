@@ -276,10 +276,11 @@ class Qwen3ForCausalLM(nn.Module):
         self, x: Tensor, cos: Tensor, sin: Tensor, kv_caches: list[tuple[Tensor, Tensor]], meta: AttentionMetadata
     ) -> Tensor:
         """The layer loop for batches above the token-split limit (prefill chunks): int8 linears on
-        the LDS-tiled MFMA GEMM (residual adds and silu * up in its epilogue), RMSNorm and the
-        q/k-norm + RoPE + KV-write as their own kernels. Returns norm(x_L), the same value as the
-        module-by-module loop; ``x`` (the embedding output) is updated in place as the residual
-        stream."""
+        the LDS-tiled MFMA GEMM (silu * up in its epilogue; the o and down projections add the
+        residual and apply the next RMSNorm, merging split-K partials in the same pass), the first
+        RMSNorm and the q/k-norm + RoPE + KV-write as their own kernels. Returns norm(x_L), the same
+        value as the module-by-module loop; ``x`` (the embedding output) is updated in place as the
+        residual stream."""
         cfg = self.cfg
         t = x.shape[0]
         layers = self.layers
@@ -292,13 +293,12 @@ class Qwen3ForCausalLM(nn.Module):
                 attn.q_norm.weight, attn.k_norm.weight, attn.q_norm.eps, cos, sin, meta.slot_mapping, k_cache, v_cache,
             )
             a = attend(q, k_cache, v_cache, meta, attn.scale).view(t, attn.q_size)
-            kernels.int8_linear(a, o.qweight, o.scale, kernels.EPI_RESIDUAL, residual=x, out=x)
             post = layer.post_attention_layernorm
-            act = kernels.int8_linear(kernels.rmsnorm(x, post.weight, post.eps), gu.qweight, gu.scale,
-                                      kernels.EPI_SILU_MUL)
-            kernels.int8_linear(act, dn.qweight, dn.scale, kernels.EPI_RESIDUAL, residual=x, out=x)
+            hn = kernels.int8_linear_add_rmsnorm(a, o.qweight, o.scale, x, post.weight, post.eps)
+            act = kernels.int8_linear(hn, gu.qweight, gu.scale, kernels.EPI_SILU_MUL)
             nxt = layers[i + 1].input_layernorm if i + 1 < len(layers) else self.norm
-            h = kernels.rmsnorm(x, nxt.weight, cfg.rms_norm_eps if nxt is self.norm else nxt.eps)
+            h = kernels.int8_linear_add_rmsnorm(act, dn.qweight, dn.scale, x, nxt.weight,
+                                                cfg.rms_norm_eps if nxt is self.norm else nxt.eps)
         return h
 
     def compute_logits(self, hidden: Tensor) -> Tensor:

@@ -57,6 +57,9 @@ def test_argument_errors_are_reported():
         "msa_paged_attention_decode", FAKE, 64, FAKE, FAKE, 16, 2, 1, 64, 16, FAKE, 1, FAKE, FAKE, 1, 16, 1, 1.0,
         FAKE, 64, NULL, 0, NULL,
     )
+    assert "null pointer" in _err(
+        "msa_int8_linear_add_rmsnorm", FAKE, 4, 64, 64, FAKE, FAKE, 64, NULL, FAKE, 1e-6, FAKE, NULL, 0, NULL
+    )
     assert "at most 4096" in _err(  # a split's keys: one block-table entry per lane of each wavefront
         "msa_paged_attention_decode", FAKE, 128 * 2, FAKE, FAKE, 16, 2, 1, 128, 16, FAKE, 1, FAKE, FAKE, 1, 4112, 1,
         1.0, FAKE, 128 * 2, NULL, 0, NULL,

@@ -12,6 +12,7 @@ from helpers import rel_l2
 
 from miniserve_amd import _native, kernels
 from oracle import int8 as oi
+from oracle import layers as ol
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -79,3 +80,24 @@ def test_gemm_residual_in_place(m, k):
     y = kernels.int8_linear(x.to(DEV), q.to(DEV), s.to(DEV)).cpu()
     assert torch.equal(rd.cpu(), r + y)  # the add itself is exact on the kernel's own product
     assert rel_l2(rd.cpu(), r + oi.int8_linear(x, q, s)) < 1e-2
+
+
+@pytest.mark.parametrize("m,n,k", [(2048, 1024, 2048), (2048, 1024, 3072), (256, 4096, 4096), (128, 1024, 3072),
+                                   (300, 2048, 1024), (64, 1024, 1024)])
+def test_linear_add_rmsnorm(m, n, k):
+    """o / down projection + residual + the next RMSNorm in one call (split-K partials merged, added
+    and normalized by one kernel when the GEMM splits) against the unfused linear and norm."""
+    q, s = oi.quantize_int8(_bf16((n, k), seed=n + 2 * k, std=0.02))
+    x = _bf16((m, k), seed=m + 5)
+    r = _bf16((m, n), seed=m + 6)
+    w = (1 + 0.1 * torch.randn(n, generator=torch.Generator().manual_seed(7))).to(torch.bfloat16)
+    xd, qd, sd, wd = x.to(DEV), q.to(DEV), s.to(DEV), w.to(DEV)
+    r1 = r.to(DEV)
+    h1 = kernels.int8_linear_add_rmsnorm(xd, qd, sd, r1, wd, 1e-6)
+    r2 = r.to(DEV)
+    kernels.int8_linear(xd, qd, sd, kernels.EPI_RESIDUAL, residual=r2, out=r2)
+    h2 = kernels.rmsnorm(r2, wd, 1e-6)
+    assert torch.equal(r1, r2)  # the merge sums the partials in the same split order
+    assert rel_l2(h1.cpu(), h2.cpu()) < 2e-3  # sums of squares in another float32 order
+    ref = ol.rms_norm(r + oi.int8_linear(x, q, s), w, 1e-6)
+    assert rel_l2(h1.cpu(), ref) < 1e-2
