@@ -87,28 +87,30 @@ __global__ __launch_bounds__(256) void int8_gemm_kernel(GemmArgs a) {
     bp[i] = a.w + (int64_t)row * a.k + kbase + bc;
     bs[i] = bf16_to_f32(a.scale[row]);
   }
-  uint4 ra0, ra1, ra2, ra3, rb0, rb1;  // the next K step's tiles, in flight during the MFMAs
-#define MSA_GEMM_LOAD(k0)                                   \
-  do {                                                      \
-    ra0 = *(const uint4*)(ap[0] + (k0));                    \
-    ra1 = *(const uint4*)(ap[1] + (k0));                    \
-    ra2 = *(const uint4*)(ap[2] + (k0));                    \
-    ra3 = *(const uint4*)(ap[3] + (k0));                    \
-    rb0 = *(const uint4*)(bp[0] + (k0));                    \
-    rb1 = *(const uint4*)(bp[1] + (k0));                    \
+  // A K step's global tiles in registers: two sets, so that a step's loads are issued two steps
+  // before its LDS store -- in flight during two steps of MFMAs.
+  uint4 ra0, ra1, ra2, ra3, rb0, rb1, sa0, sa1, sa2, sa3, sb0, sb1;
+#define MSA_GEMM_LOAD(p, k0)                  \
+  do {                                        \
+    p##a0 = *(const uint4*)(ap[0] + (k0));    \
+    p##a1 = *(const uint4*)(ap[1] + (k0));    \
+    p##a2 = *(const uint4*)(ap[2] + (k0));    \
+    p##a3 = *(const uint4*)(ap[3] + (k0));    \
+    p##b0 = *(const uint4*)(bp[0] + (k0));    \
+    p##b1 = *(const uint4*)(bp[1] + (k0));    \
   } while (0)
-#define MSA_GEMM_STORE(buf)                                                           \
-  do {                                                                                \
-    uint16_t* A_ = As + (buf) * kGBM * kGLd + ar * kGLd + ac;                         \
-    *(uint4*)(A_) = ra0;                                                              \
-    *(uint4*)(A_ + 32 * kGLd) = ra1;                                                  \
-    *(uint4*)(A_ + 64 * kGLd) = ra2;                                                  \
-    *(uint4*)(A_ + 96 * kGLd) = ra3;                                                  \
-    uint16_t* B_ = Bs + (buf) * kGBN * kGLd + br * kGLd + bc;                         \
-    *(bf16x8*)(B_) = dequant8(rb0.x, rb0.y, bs[0]);                              \
-    *(bf16x8*)(B_ + 8) = dequant8(rb0.z, rb0.w, bs[0]);                          \
-    *(bf16x8*)(B_ + 64 * kGLd) = dequant8(rb1.x, rb1.y, bs[1]);                  \
-    *(bf16x8*)(B_ + 64 * kGLd + 8) = dequant8(rb1.z, rb1.w, bs[1]);              \
+#define MSA_GEMM_STORE(p, buf)                                              \
+  do {                                                                      \
+    uint16_t* A_ = As + (buf) * kGBM * kGLd + ar * kGLd + ac;               \
+    *(uint4*)(A_) = p##a0;                                                  \
+    *(uint4*)(A_ + 32 * kGLd) = p##a1;                                      \
+    *(uint4*)(A_ + 64 * kGLd) = p##a2;                                      \
+    *(uint4*)(A_ + 96 * kGLd) = p##a3;                                      \
+    uint16_t* B_ = Bs + (buf) * kGBN * kGLd + br * kGLd + bc;               \
+    *(bf16x8*)(B_) = dequant8(p##b0.x, p##b0.y, bs[0]);                     \
+    *(bf16x8*)(B_ + 8) = dequant8(p##b0.z, p##b0.w, bs[0]);                 \
+    *(bf16x8*)(B_ + 64 * kGLd) = dequant8(p##b1.x, p##b1.y, bs[1]);         \
+    *(bf16x8*)(B_ + 64 * kGLd + 8) = dequant8(p##b1.z, p##b1.w, bs[1]);     \
   } while (0)
 
   f32x4 acc[4][4];
@@ -117,35 +119,46 @@ __global__ __launch_bounds__(256) void int8_gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+#define MSA_GEMM_COMPUTE(cur)                                                                        \
+  do {                                                                                               \
+    const uint16_t* A = As + (cur) * kGBM * kGLd + (wm * 64 + j) * kGLd + g * 8;                      \
+    const uint16_t* B = Bs + (cur) * kGBN * kGLd + (wn * 64 + j) * kGLd + g * 8;                      \
+    _Pragma("unroll") for (int ks = 0; ks < 2; ++ks) {                                               \
+      bf16x8 af[4], bfr[4];                                                                          \
+      _Pragma("unroll") for (int t = 0; t < 4; ++t) {                                                \
+        af[t] = *(const bf16x8*)(A + t * 16 * kGLd + ks * 32);                                       \
+        bfr[t] = *(const bf16x8*)(B + t * 16 * kGLd + ks * 32);                                      \
+      }                                                                                              \
+      _Pragma("unroll") for (int mt = 0; mt < 4; ++mt)                                               \
+        _Pragma("unroll") for (int nt = 0; nt < 4; ++nt)                                             \
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt], bfr[nt], acc[mt][nt], 0, 0, 0); \
+    }                                                                                                \
+  } while (0)
+
+  // Step kt computes from LDS buffer kt & 1 while step kt + 1's tiles wait in registers (set
+  // (kt + 1) & 1) and step kt + 2's are requested into the other set; then step kt + 1 is stored.
+  // Steps past nk load clamped addresses (the last step again) and are never stored.
   const int nk = a.k_per / kGBK;
-  MSA_GEMM_LOAD(0);
-  MSA_GEMM_STORE(0);
+  const int klast = (nk - 1) * kGBK;
+  MSA_GEMM_LOAD(r, 0);
+  MSA_GEMM_LOAD(s, min(kGBK, klast));
+  MSA_GEMM_STORE(r, 0);
   __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    const bool more = kt + 1 < nk;
-    if (more) MSA_GEMM_LOAD((kt + 1) * kGBK);
-    const uint16_t* A = As + cur * kGBM * kGLd + (wm * 64 + j) * kGLd + g * 8;
-    const uint16_t* B = Bs + cur * kGBN * kGLd + (wn * 64 + j) * kGLd + g * 8;
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      bf16x8 af[4], bfr[4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        af[t] = *(const bf16x8*)(A + t * 16 * kGLd + ks * 32);
-        bfr[t] = *(const bf16x8*)(B + t * 16 * kGLd + ks * 32);
-      }
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-        for (int nt = 0; nt < 4; ++nt)
-          acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt], bfr[nt], acc[mt][nt], 0, 0, 0);
-    }
-    if (more) MSA_GEMM_STORE(cur ^ 1);
+  int kt = 0;
+  for (; kt + 2 <= nk; kt += 2) {
+    MSA_GEMM_LOAD(r, min((kt + 2) * kGBK, klast));
+    MSA_GEMM_COMPUTE(0);
+    MSA_GEMM_STORE(s, 1);  // step kt + 1 (exists: kt + 2 <= nk)
+    __syncthreads();
+    MSA_GEMM_LOAD(s, min((kt + 3) * kGBK, klast));
+    MSA_GEMM_COMPUTE(1);
+    if (kt + 2 < nk) MSA_GEMM_STORE(r, 0);  // step kt + 2
     __syncthreads();
   }
+  if (kt < nk) MSA_GEMM_COMPUTE(0);  // odd nk: the last step, stored at the end of the loop
 #undef MSA_GEMM_LOAD
 #undef MSA_GEMM_STORE
+#undef MSA_GEMM_COMPUTE
 
   // lane (g, j) of tile (mt, nt): tokens m0 + wm*64 + mt*16 + 4g + i, LDS weight row wn*64 + nt*16 + j
 #pragma unroll
