@@ -481,6 +481,7 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(PrefillArgs a) {
   const int qi_c = qvalid ? qi : nnew - 1;
   const int qpos = ncached + qi_c;
   const int wave_last = ncached + min(tstart + st * 16 + 15, nnew - 1);
+  const int wave_first = ncached + min(tstart + st * 16, nnew - 1);  // the wave's lowest query position
 
   bf16x8 qfrag[4];
   {
@@ -494,22 +495,35 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(PrefillArgs a) {
   const int32_t* btr = a.bt + (int64_t)seq * a.max_blocks;
   const int64_t tok_stride = (int64_t)a.kv_heads * kHeadDim;
 
-  // Loader role: keys 2la and 2la + 1 of the tile, 8-wide dim chunks lb and lb + 8.
+  // Loader role: keys 2la and 2la + 1 of the tile (both in block tile * 4 + la / 8), 8-wide dim
+  // chunks lb and lb + 8. A tile's table entry is read one tile before its keys and values, so
+  // the keys never wait on a table read; every load is issued unconditionally (the table index
+  // clamped into the row, a dead key's address masked to the cache's first row) and a dead key's
+  // value is zeroed where it is stored, so the probability 0 it gets multiplies a zero.
   const int la = threadIdx.x & 31, lb = threadIdx.x >> 5;
   uint4 kr[2][2], vr[2][2];  // [key rr][chunk cc]
-  auto load_tile = [&](int tile) {
+  uint32_t vmask[2];         // all ones for a live key, 0 for a dead one
+  auto table_entry = [&](int tile) {
+    return btr[min(tile * (kKeyTile / kBlock) + la / 8, a.max_blocks - 1)];
+  };
+  auto load_tile = [&](int tile, int phys) {
+    phys = ((uint32_t)phys < (uint64_t)a.num_blocks) ? phys : 0;
 #pragma unroll
     for (int rr = 0; rr < 2; ++rr) {
       const int key = tile * kKeyTile + 2 * la + rr;
       const bool ok = key < kend && key / kBlock < a.max_blocks;
-      int phys = ok ? btr[key / kBlock] : 0;
-      phys = ((uint32_t)phys < (uint64_t)a.num_blocks) ? phys : 0;
-      const int64_t off = ((int64_t)phys * kBlock + key % kBlock) * tok_stride + (int64_t)kvh * kHeadDim + 8 * lb;
+      const int64_t mask = -(int64_t)ok;
+      const int64_t off =
+          (((int64_t)phys * kBlock + key % kBlock) * tok_stride + (int64_t)kvh * kHeadDim + 8 * lb) & mask;
 #pragma unroll
       for (int cc = 0; cc < 2; ++cc) {
-        kr[rr][cc] = ok ? *(const uint4*)(a.kc + off + 64 * cc) : uint4{0, 0, 0, 0};
-        vr[rr][cc] = ok ? *(const uint4*)(a.vc + off + 64 * cc) : uint4{0, 0, 0, 0};
+        // loaded as vector values, not struct copies (which the compiler keeps in scratch)
+        const u32x4 k = *(const u32x4*)(a.kc + off + (64 * cc & mask));
+        const u32x4 v = *(const u32x4*)(a.vc + off + (64 * cc & mask));
+        kr[rr][cc] = uint4{k.x, k.y, k.z, k.w};
+        vr[rr][cc] = uint4{v.x, v.y, v.z, v.w};
       }
+      vmask[rr] = (uint32_t)mask;  // applied where the values are stored, not while they load
     }
   };
   auto store_tile = [&](int buf) {
@@ -522,7 +536,7 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(PrefillArgs a) {
 #pragma unroll
       for (int e = 0; e < 8; ++e)
         *(uint32_t*)&V[(8 * lb + 64 * cc + e) * kVtStride + 2 * la] =
-            (uint32_t)elem16(vr[0][cc], e) | ((uint32_t)elem16(vr[1][cc], e) << 16);
+            ((uint32_t)elem16(vr[0][cc], e) & vmask[0]) | (((uint32_t)elem16(vr[1][cc], e) & vmask[1]) << 16);
     }
   };
 
@@ -533,9 +547,11 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(PrefillArgs a) {
 
   // Pipeline: tile t is computed from LDS buffer t % 2 while the registers receive tile t + 1;
   // those are written to the other buffer after the MFMAs, then tile t + 2 is requested.
-  load_tile(0);
+  load_tile(0, table_entry(0));
+  const int ph1 = table_entry(1);
   store_tile(0);
-  if (ntiles > 1) load_tile(1);
+  if (ntiles > 1) load_tile(1, ph1);
+  int ph_next = table_entry(2);  // the entry of tile + 2 at the top of iteration tile
   __syncthreads();
   for (int tile = 0; tile < ntiles; ++tile) {
     const int buf = tile & 1;
@@ -554,29 +570,41 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(PrefillArgs a) {
         }
       }
       float s16[16];
+      if (key0 + kKeyTile - 1 <= wave_first) {  // wave-uniform: the tile is below the diagonal
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
+        for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const int key = key0 + mt * 16 + 4 * grp + rr;
-          s16[mt * 4 + rr] = key <= qpos ? sT[mt][rr] * a.scale_log2 : -INFINITY;
-        }
+          for (int rr = 0; rr < 4; ++rr) s16[mt * 4 + rr] = sT[mt][rr] * a.scale_log2;
+      } else {
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) {
+            const int key = key0 + mt * 16 + 4 * grp + rr;
+            s16[mt * 4 + rr] = key <= qpos ? sT[mt][rr] * a.scale_log2 : -INFINITY;
+          }
+      }
       float bm = s16[0];
 #pragma unroll
       for (int e = 1; e < 16; ++e) bm = fmaxf(bm, s16[e]);
       bm = xrow_max(bm);
       const float mn = fmaxf(m, bm);  // finite: key 0 is visible to every query
-      const float alpha = exp2f(m - mn);
-      m = mn;
-      l *= alpha;
+      // Rescale only when some row's maximum grew: elsewhere the factor is exp2(0) = 1 exactly.
+      if (__builtin_amdgcn_ballot_w64(mn > m)) {
+        const float alpha = __builtin_amdgcn_exp2f(m - mn);  // 0 on the first tile (m = -inf)
+        l *= alpha;
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
+        for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
+      }
+      m = mn;
 #pragma unroll
       for (int h = 0; h < 2; ++h) {  // keys 32h .. 32h + 31: this lane's 8 are (2h + t) * 16 + 4grp + rr
         bf16x8 pb;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float p = exp2f(s16[8 * h + e] - mn);
+          // the hardware exp2: arguments are <= 0 and results below 2^-126 are negligible
+          // against the row's largest weight, 1
+          const float p = __builtin_amdgcn_exp2f(s16[8 * h + e] - mn);
           l += p;
           pb[e] = (__bf16)p;
         }
@@ -592,7 +620,8 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(PrefillArgs a) {
     }
     if (tile + 1 < ntiles) {
       store_tile(buf ^ 1);  // buffer of tile t - 1: every wavefront passed the barrier after it
-      if (tile + 2 < ntiles) load_tile(tile + 2);
+      if (tile + 2 < ntiles) load_tile(tile + 2, ph_next);
+      ph_next = table_entry(tile + 3);
     }
     __syncthreads();
   }
