@@ -46,9 +46,15 @@ def hipcc() -> str:
     return path
 
 
+# Per-file extra flags. attention.hip: keep MFMA accumulators in ordinary VGPRs -- the prefill
+# kernel rescales its output accumulators between MFMAs every key tile, and in accumulation
+# registers each rescale costs a copy out and a copy back.
+EXTRA_FLAGS = {"attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+
+
 def _compile(src: str) -> Path:
     obj = BUILD / (Path(src).stem + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
+    cmd = [hipcc(), *HIPCC_FLAGS, *EXTRA_FLAGS.get(src, []), "-c", str(CSRC / src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{res.stderr[-6000:]}")

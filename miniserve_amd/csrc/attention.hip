@@ -455,11 +455,6 @@ struct PrefillArgs {
   int64_t ldo;
 };
 
-__device__ __forceinline__ uint16_t elem16(const uint4& v, int e) {
-  const uint32_t w = e < 2 ? v.x : e < 4 ? v.y : e < 6 ? v.z : v.w;
-  return (uint16_t)((e & 1) ? (w >> 16) : (w & 0xffff));
-}
-
 template <int G>
 __global__ __launch_bounds__(256) void paged_prefill_kernel(PrefillArgs a) {
   constexpr int kSub = 4 / G;       // 16-token query sub-tiles per workgroup
@@ -529,14 +524,23 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(PrefillArgs a) {
   auto store_tile = [&](int buf) {
     uint16_t* K = Ks + buf * kKsTile;
     uint16_t* V = Vt + buf * kVtTile;
+    const uint32_t live = (vmask[1] & 0xffff0000u) | (vmask[0] & 0x0000ffffu);
+    const uint32_t sel_lo = (0x05040100u & live) | (0x0c0c0c0cu & ~live);
+    const uint32_t sel_hi = (0x07060302u & live) | (0x0c0c0c0cu & ~live);
 #pragma unroll
     for (int cc = 0; cc < 2; ++cc) {
 #pragma unroll
       for (int rr = 0; rr < 2; ++rr) *(uint4*)&K[(2 * la + rr) * kKsStride + 8 * lb + 64 * cc] = kr[rr][cc];
+      // V^T word of dim 2i (2i + 1): the low (high) halves of dword i of keys 2la and 2la + 1, one
+      // byte permute each; selector bytes 0x0c give zero bytes for a dead key.
+      const uint32_t v0[4] = {vr[0][cc].x, vr[0][cc].y, vr[0][cc].z, vr[0][cc].w};
+      const uint32_t v1[4] = {vr[1][cc].x, vr[1][cc].y, vr[1][cc].z, vr[1][cc].w};
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        *(uint32_t*)&V[(8 * lb + 64 * cc + e) * kVtStride + 2 * la] =
-            ((uint32_t)elem16(vr[0][cc], e) & vmask[0]) | (((uint32_t)elem16(vr[1][cc], e) & vmask[1]) << 16);
+      for (int i = 0; i < 4; ++i) {
+        uint32_t* row = (uint32_t*)&V[(8 * lb + 64 * cc + 2 * i) * kVtStride + 2 * la];
+        row[0] = __builtin_amdgcn_perm(v1[i], v0[i], sel_lo);
+        row[kVtStride / 2] = __builtin_amdgcn_perm(v1[i], v0[i], sel_hi);
+      }
     }
   };
 
