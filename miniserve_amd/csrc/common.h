@@ -36,6 +36,11 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
   return __builtin_bit_cast(uint16_t, b);
 }
 __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+// SiLU x / (1 + e^-x) from the hardware exp2 and reciprocal (each within 1 ulp; the result within
+// ~3e-7 relative, far below the bf16 rounding that follows it). Large negative x gives -0.
+__device__ __forceinline__ float silu_f32(float x) {
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * kLog2e));
+}
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x8_t __attribute__((ext_vector_type(8)));
 // Two floats -> a bf16 pair (round to nearest even) in one v_cvt_pk_bf16_f32; converting the

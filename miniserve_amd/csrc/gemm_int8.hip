@@ -180,7 +180,7 @@ __global__ __launch_bounds__(256) void int8_gemm_kernel(GemmArgs a) {
           const int col = nb * 64 + wn * 32 + nt * 16 + j;
           if (col >= a.n / 2) continue;
           const float gt = round_bf16(acc[mt][nt][i]), up = round_bf16(acc[mt][nt + 2][i]);
-          a.y[(int64_t)tok * a.ldy + col] = f32_to_bf16(round_bf16(gt / (1.0f + expf(-gt))) * up);
+          a.y[(int64_t)tok * a.ldy + col] = f32_to_bf16(round_bf16(silu_f32(gt)) * up);
         }
       } else {
 #pragma unroll

@@ -47,7 +47,7 @@ struct SkinnyArgs {
 __device__ __forceinline__ float silu_mul(float gate_acc, float up_acc) {
   const float g = round_bf16(gate_acc);
   const float u = round_bf16(up_acc);
-  return round_bf16(g / (1.0f + expf(-g))) * u;
+  return round_bf16(silu_f32(g)) * u;
 }
 
 // Weight row of n-tile nt for lane row j in block nblk.

@@ -314,7 +314,7 @@ __global__ __launch_bounds__(64 * KW) __attribute__((amdgpu_waves_per_eu(1, 1)))
       float o;
       if constexpr (SILU) {
         const float gt = round_bf16(v0[i] * (rf[i] * s0)), up = round_bf16(v1[i] * (rf[i] * s1));
-        o = round_bf16(gt / (1.0f + expf(-gt))) * up;
+        o = round_bf16(silu_f32(gt)) * up;
       } else if constexpr (EPI == DL_EPI_RESIDUAL) {
         o = round_bf16(v0[i] * (rf[i] * s0)) + bf16_to_f32(rres[uu][i]);
       } else {

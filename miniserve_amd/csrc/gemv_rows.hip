@@ -88,7 +88,7 @@ struct RowsArgs {
 __device__ __forceinline__ float silu_mul_rows(float gate_acc, float up_acc) {
   const float g = round_bf16(gate_acc);
   const float u = round_bf16(up_acc);
-  return round_bf16(g / (1.0f + expf(-g))) * u;
+  return round_bf16(silu_f32(g)) * u;
 }
 
 // Sum over aligned groups of TPT lanes (TPT = 16, 32 or 64); every lane of a group gets the total.
