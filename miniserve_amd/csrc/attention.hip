@@ -431,12 +431,16 @@ __global__ __launch_bounds__(kHeadDim) void paged_decode_reduce_kernel(DecodeArg
 
 // ---------------------------------------------------------------------------------------------
 
-constexpr int kKeyTile = 64;             // keys per LDS tile
+constexpr int kKeyTile = 32;             // keys per LDS tile
 constexpr int kKsStride = kHeadDim + 8;  // bf16 elements per K row in LDS
 constexpr int kVtStride = kKeyTile + 4;  // bf16 elements per transposed V row in LDS
 constexpr int kKsTile = kKeyTile * kKsStride;
 constexpr int kVtTile = kHeadDim * kVtStride;
-constexpr size_t kPrefillLds = (size_t)2 * (kKsTile + kVtTile) * 2;  // two buffers of K and V^T
+constexpr int kKeyGroups = 2;  // groups of four wavefronts splitting a workgroup's key tiles
+// Per key group two buffers of K and V^T: 71,680 bytes, two workgroups per CU.
+constexpr size_t kPrefillLds = (size_t)kKeyGroups * 2 * (kKsTile + kVtTile) * 2;
+constexpr int kXchFloats = 34 * 64;  // per wavefront at the merge: 32 accumulators, m, l per lane
+static_assert((size_t)4 * kXchFloats * 4 <= kPrefillLds, "merge exchange fits the tile buffers");
 
 struct PrefillArgs {
   const uint16_t* q;
@@ -455,18 +459,24 @@ struct PrefillArgs {
   int64_t ldo;
 };
 
+// Two key groups of four wavefronts: group kg takes key tiles kg, kg + 2, ... of the workgroup's
+// query tile, with its own double-buffered K / V^T tiles, and hands its softmax state to group 0
+// through LDS at the end -- twice the wavefronts in flight and half the chain of key tiles of the
+// longest query tile.
 template <int G>
-__global__ __launch_bounds__(256) void paged_prefill_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void paged_prefill_kernel(PrefillArgs a) {
   constexpr int kSub = 4 / G;       // 16-token query sub-tiles per workgroup
   constexpr int kQTok = 16 * kSub;  // query tokens per workgroup
   extern __shared__ __attribute__((aligned(16))) uint16_t psm[];
-  uint16_t* Ks = psm;                // [2][kKeyTile][kKsStride]
-  uint16_t* Vt = psm + 2 * kKsTile;  // [2][kHeadDim][kVtStride]
+  const int kg = __builtin_amdgcn_readfirstlane(threadIdx.x >> 8);  // key group
+  const int tg = threadIdx.x & 255;                                  // thread within the key group
+  uint16_t* Ks = psm + kg * 2 * (kKsTile + kVtTile);  // [2][kKeyTile][kKsStride]
+  uint16_t* Vt = Ks + 2 * kKsTile;                     // [2][kHeadDim][kVtStride]
 
   const int wi = blockIdx.x, kvh = blockIdx.y;
   const int seq = a.work[2 * wi], tstart = a.work[2 * wi + 1];
   const int flat = a.seq_info[3 * seq], nnew = a.seq_info[3 * seq + 1], ncached = a.seq_info[3 * seq + 2];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = tg >> 6;  // wavefront within the key group
   const int g = wave % G, st = wave / G;
   const int head = kvh * G + g;
   const int j = lane & 15, grp = lane >> 4;
@@ -487,17 +497,19 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(PrefillArgs a) {
 
   const int kend = ncached + min(tstart + kQTok, nnew);
   const int ntiles = (kend + kKeyTile - 1) / kKeyTile;
+  const int niter = (ntiles + kKeyGroups - 1) / kKeyGroups;  // tiles per key group (group 1 may idle once)
   const int32_t* btr = a.bt + (int64_t)seq * a.max_blocks;
   const int64_t tok_stride = (int64_t)a.kv_heads * kHeadDim;
 
-  // Loader role: keys 2la and 2la + 1 of the tile (both in block tile * 4 + la / 8), 8-wide dim
-  // chunks lb and lb + 8. A tile's table entry is read one tile before its keys and values, so
-  // the keys never wait on a table read; every load is issued unconditionally (the table index
-  // clamped into the row, a dead key's address masked to the cache's first row) and a dead key's
-  // value is zeroed where it is stored, so the probability 0 it gets multiplies a zero.
-  const int la = threadIdx.x & 31, lb = threadIdx.x >> 5;
-  uint4 kr[2][2], vr[2][2];  // [key rr][chunk cc]
-  uint32_t vmask[2];         // all ones for a live key, 0 for a dead one
+  // Loader role within the key group: keys 2la and 2la + 1 of the tile (both in block
+  // tile * 2 + la / 8), 8-wide dim chunk lb. A tile's table entry is read one tile before its keys
+  // and values, so the keys never wait on a table read; every load is issued unconditionally (the
+  // table index clamped into the row, a dead key's address masked to the cache's first row) and a
+  // dead key's value is zeroed where it is stored, so the probability 0 it gets multiplies a zero.
+  const int la = tg & 15, lb = tg >> 4;
+  uint4 kr[2], vr[2];  // [key rr]
+  uint32_t vmask[2];   // all ones for a live key, 0 for a dead one
+  auto tile_of = [&](int i) { return kg + kKeyGroups * i; };  // the group's i-th tile
   auto table_entry = [&](int tile) {
     return btr[min(tile * (kKeyTile / kBlock) + la / 8, a.max_blocks - 1)];
   };
@@ -510,14 +522,11 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(PrefillArgs a) {
       const int64_t mask = -(int64_t)ok;
       const int64_t off =
           (((int64_t)phys * kBlock + key % kBlock) * tok_stride + (int64_t)kvh * kHeadDim + 8 * lb) & mask;
-#pragma unroll
-      for (int cc = 0; cc < 2; ++cc) {
-        // loaded as vector values, not struct copies (which the compiler keeps in scratch)
-        const u32x4 k = *(const u32x4*)(a.kc + off + (64 * cc & mask));
-        const u32x4 v = *(const u32x4*)(a.vc + off + (64 * cc & mask));
-        kr[rr][cc] = uint4{k.x, k.y, k.z, k.w};
-        vr[rr][cc] = uint4{v.x, v.y, v.z, v.w};
-      }
+      // loaded as vector values, not struct copies (which the compiler keeps in scratch)
+      const u32x4 k = *(const u32x4*)(a.kc + off);
+      const u32x4 v = *(const u32x4*)(a.vc + off);
+      kr[rr] = uint4{k.x, k.y, k.z, k.w};
+      vr[rr] = uint4{v.x, v.y, v.z, v.w};
       vmask[rr] = (uint32_t)mask;  // applied where the values are stored, not while they load
     }
   };
@@ -528,19 +537,16 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(PrefillArgs a) {
     const uint32_t sel_lo = (0x05040100u & live) | (0x0c0c0c0cu & ~live);
     const uint32_t sel_hi = (0x07060302u & live) | (0x0c0c0c0cu & ~live);
 #pragma unroll
-    for (int cc = 0; cc < 2; ++cc) {
+    for (int rr = 0; rr < 2; ++rr) *(uint4*)&K[(2 * la + rr) * kKsStride + 8 * lb] = kr[rr];
+    // V^T word of dim 8lb + 2i (+ 1): the low (high) halves of dword i of keys 2la and 2la + 1, one
+    // byte permute each; selector bytes 0x0c give zero bytes for a dead key.
+    const uint32_t v0[4] = {vr[0].x, vr[0].y, vr[0].z, vr[0].w};
+    const uint32_t v1[4] = {vr[1].x, vr[1].y, vr[1].z, vr[1].w};
 #pragma unroll
-      for (int rr = 0; rr < 2; ++rr) *(uint4*)&K[(2 * la + rr) * kKsStride + 8 * lb + 64 * cc] = kr[rr][cc];
-      // V^T word of dim 2i (2i + 1): the low (high) halves of dword i of keys 2la and 2la + 1, one
-      // byte permute each; selector bytes 0x0c give zero bytes for a dead key.
-      const uint32_t v0[4] = {vr[0][cc].x, vr[0][cc].y, vr[0][cc].z, vr[0][cc].w};
-      const uint32_t v1[4] = {vr[1][cc].x, vr[1][cc].y, vr[1][cc].z, vr[1][cc].w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        uint32_t* row = (uint32_t*)&V[(8 * lb + 64 * cc + 2 * i) * kVtStride + 2 * la];
-        row[0] = __builtin_amdgcn_perm(v1[i], v0[i], sel_lo);
-        row[kVtStride / 2] = __builtin_amdgcn_perm(v1[i], v0[i], sel_hi);
-      }
+    for (int i = 0; i < 4; ++i) {
+      uint32_t* row = (uint32_t*)&V[(8 * lb + 2 * i) * kVtStride + 2 * la];
+      row[0] = __builtin_amdgcn_perm(v1[i], v0[i], sel_lo);
+      row[kVtStride / 2] = __builtin_amdgcn_perm(v1[i], v0[i], sel_hi);
     }
   };
 
@@ -549,23 +555,24 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(PrefillArgs a) {
   for (int dt = 0; dt < 8; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m = -INFINITY, l = 0.f;
 
-  // Pipeline: tile t is computed from LDS buffer t % 2 while the registers receive tile t + 1;
-  // those are written to the other buffer after the MFMAs, then tile t + 2 is requested.
-  load_tile(0, table_entry(0));
-  const int ph1 = table_entry(1);
+  // Pipeline per key group: its tile i is computed from LDS buffer i % 2 while the registers
+  // receive its tile i + 1; those are written to the other buffer after the MFMAs, then tile i + 2
+  // is requested. Both groups run niter iterations, so every barrier is reached by all wavefronts.
+  load_tile(tile_of(0), table_entry(tile_of(0)));
+  const int ph1 = table_entry(tile_of(1));
   store_tile(0);
-  if (ntiles > 1) load_tile(1, ph1);
-  int ph_next = table_entry(2);  // the entry of tile + 2 at the top of iteration tile
+  if (niter > 1) load_tile(tile_of(1), ph1);
+  int ph_next = table_entry(tile_of(2));  // the entry of the group's tile i + 2 at the top of iteration i
   __syncthreads();
-  for (int tile = 0; tile < ntiles; ++tile) {
-    const int buf = tile & 1;
-    const int key0 = tile * kKeyTile;
-    if (key0 <= wave_last) {  // else every query of this wavefront precedes the tile
+  for (int i = 0; i < niter; ++i) {
+    const int buf = i & 1;
+    const int key0 = tile_of(i) * kKeyTile;
+    if (key0 <= wave_last) {  // else every query of this wavefront precedes the tile (or it is past kend)
       const uint16_t* K = Ks + buf * kKsTile;
       const uint16_t* V = Vt + buf * kVtTile;
-      f32x4 sT[4];
+      f32x4 sT[2];
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
+      for (int mt = 0; mt < 2; ++mt) {
         sT[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
@@ -573,70 +580,92 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(PrefillArgs a) {
           sT[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qfrag[ks], sT[mt], 0, 0, 0);
         }
       }
-      float s16[16];
+      // this lane's 8 keys: mt * 16 + 4grp + rr (s8[mt * 4 + rr])
+      float s8[8];
       if (key0 + kKeyTile - 1 <= wave_first) {  // wave-uniform: the tile is below the diagonal
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
+        for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-          for (int rr = 0; rr < 4; ++rr) s16[mt * 4 + rr] = sT[mt][rr] * a.scale_log2;
+          for (int rr = 0; rr < 4; ++rr) s8[mt * 4 + rr] = sT[mt][rr] * a.scale_log2;
       } else {
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
+        for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
           for (int rr = 0; rr < 4; ++rr) {
             const int key = key0 + mt * 16 + 4 * grp + rr;
-            s16[mt * 4 + rr] = key <= qpos ? sT[mt][rr] * a.scale_log2 : -INFINITY;
+            s8[mt * 4 + rr] = key <= qpos ? sT[mt][rr] * a.scale_log2 : -INFINITY;
           }
       }
-      float bm = s16[0];
+      float bm = s8[0];
 #pragma unroll
-      for (int e = 1; e < 16; ++e) bm = fmaxf(bm, s16[e]);
+      for (int e = 1; e < 8; ++e) bm = fmaxf(bm, s8[e]);
       bm = xrow_max(bm);
-      const float mn = fmaxf(m, bm);  // finite: key 0 is visible to every query
+      // group 0 sees key 0 first, so its maximum is finite from the first tile on; a group-1
+      // wavefront whose first visible tile masks a whole row keeps -inf there and adds zeros
+      const float mn = fmaxf(m, bm);
       // Rescale only when some row's maximum grew: elsewhere the factor is exp2(0) = 1 exactly.
       if (__builtin_amdgcn_ballot_w64(mn > m)) {
-        const float alpha = __builtin_amdgcn_exp2f(m - mn);  // 0 on the first tile (m = -inf)
+        const float alpha = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m - mn);  // 0 from m = -inf
         l *= alpha;
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
       }
       m = mn;
+      bf16x8 pb;
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {  // keys 32h .. 32h + 31: this lane's 8 are (2h + t) * 16 + 4grp + rr
-        bf16x8 pb;
+      for (int e = 0; e < 8; ++e) {
+        // the hardware exp2: arguments are <= 0 and results below 2^-126 are negligible against
+        // the row's largest weight, 1; a row still at -inf gets 0
+        const float p = mn == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s8[e] - mn);
+        l += p;
+        pb[e] = (__bf16)p;
+      }
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          // the hardware exp2: arguments are <= 0 and results below 2^-126 are negligible
-          // against the row's largest weight, 1
-          const float p = __builtin_amdgcn_exp2f(s16[8 * h + e] - mn);
-          l += p;
-          pb[e] = (__bf16)p;
-        }
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) {
-          const uint16_t* vrow = V + (dt * 16 + j) * kVtStride + 32 * h + 4 * grp;
-          const uint2 v0 = *(const uint2*)vrow;
-          const uint2 v1 = *(const uint2*)(vrow + 16);
-          const bf16x8 va = __builtin_bit_cast(bf16x8, uint4{v0.x, v0.y, v1.x, v1.y});
-          acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb, acc[dt], 0, 0, 0);
-        }
+      for (int dt = 0; dt < 8; ++dt) {
+        const uint16_t* vrow = V + (dt * 16 + j) * kVtStride + 4 * grp;
+        const uint2 v0 = *(const uint2*)vrow;
+        const uint2 v1 = *(const uint2*)(vrow + 16);
+        const bf16x8 va = __builtin_bit_cast(bf16x8, uint4{v0.x, v0.y, v1.x, v1.y});
+        acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb, acc[dt], 0, 0, 0);
       }
     }
-    if (tile + 1 < ntiles) {
-      store_tile(buf ^ 1);  // buffer of tile t - 1: every wavefront passed the barrier after it
-      if (tile + 2 < ntiles) load_tile(tile + 2, ph_next);
-      ph_next = table_entry(tile + 3);
+    if (i + 1 < niter) {
+      store_tile(buf ^ 1);  // buffer of the group's tile i - 1: every wavefront passed the barrier after it
+      if (i + 2 < niter) load_tile(tile_of(i + 2), ph_next);
+      ph_next = table_entry(tile_of(i + 3));
     }
     __syncthreads();
   }
-  l = xrow_sum(l);
+
+  // Merge: group 1 leaves its state in LDS (over the tile buffers, free after the last barrier);
+  // group 0 combines it with its own, lane by lane (the two groups' lanes hold the same rows and
+  // dims), and writes the output.
+  float* xch = (float*)psm + wave * kXchFloats;
+  if (kg == 1) {
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) xch[(dt * 4 + r) * 64 + lane] = acc[dt][r];
+    xch[32 * 64 + lane] = m;
+    xch[33 * 64 + lane] = l;
+  }
+  __syncthreads();
+  if (kg == 1) return;
+  const float m1 = xch[32 * 64 + lane], l1 = xch[33 * 64 + lane];
+  const float mm = fmaxf(m, m1);  // finite: group 0 saw key 0
+  const float f0 = __builtin_amdgcn_exp2f(m - mm);
+  const float f1 = m1 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m1 - mm);
+  l = xrow_sum(l * f0 + l1 * f1);
   if (!qvalid) return;
   const float inv = 1.0f / l;
   uint16_t* orow = a.out + (int64_t)(flat + qi) * a.ldo + (int64_t)head * kHeadDim;
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) {
+    float o[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) o[r] = (acc[dt][r] * f0 + xch[(dt * 4 + r) * 64 + lane] * f1) * inv;
     const int d = dt * 16 + 4 * grp;
-    *(uint2*)(orow + d) = uint2{pack_bf16x2(acc[dt][0] * inv, acc[dt][1] * inv), pack_bf16x2(acc[dt][2] * inv, acc[dt][3] * inv)};
+    *(uint2*)(orow + d) = uint2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
   }
 }
 
@@ -650,7 +679,7 @@ static int launch_prefill(const PrefillArgs& a, dim3 grid, hipStream_t s) {
     if (e != hipSuccess) return fail(MSA_ERR_LAUNCH, std::string("hipFuncSetAttribute: ") + hipGetErrorString(e));
     attr_set = true;
   }
-  hipLaunchKernelGGL(paged_prefill_kernel<G>, grid, dim3(256), kPrefillLds, s, a);
+  hipLaunchKernelGGL(paged_prefill_kernel<G>, grid, dim3(512), kPrefillLds, s, a);
   return MSA_OK;
 }
 
