@@ -489,28 +489,35 @@ __global__ __launch_bounds__(64 * W) void lm_head_argmax_kernel(RowsArgs a) {
   const int j = lane & 15, g = lane >> 4;
 
   const int ntiles = (a.n + 15) / 16;
-  const int nch = a.k / CH;  // a multiple of PF (the host picks PF)
+  const int nch = a.k / CH;  // a multiple of 2 * PF for PF > 1 (the host picks PF)
   const int stride = gridDim.x * W;
   const int first = blockIdx.x * W + wave;
   // The load cursor runs PF chunks ahead of the MFMAs across tile boundaries (the wave's tiles are
-  // first, first + stride, ...), so the ring never drains between tiles; chunk c of every tile
-  // lands in ring slot c % PF because PF divides the chunks per tile.
+  // first, first + stride, ...), so the rings never drain between tiles; every tile starts on
+  // ring a because 2 * PF divides the chunks per tile.
   auto row_ptr = [&](int tile) {
     const int row = tile * 16 + j;
     return (const uint16_t*)a.w + (int64_t)(row < a.n ? row : a.n - 1) * a.k + g * 8;
   };
+  // Two rings of PF chunks: one group of PF chunks is multiplied from one ring while the next
+  // group loads into the other, so no register holding a pending load is ever copied (which
+  // would make the compiler wait for the whole ring). Loads past the wave's last tile read row
+  // n - 1 (row_ptr clamps) and are never used; they are unconditional so that the compiler's
+  // in-order load counting waits for one slot at a time.
   int ld_tile = first, ld_c = 0;
   const uint16_t* ld_p = row_ptr(ld_tile);
-  uint4 wv[PF];
-#pragma unroll
-  for (int c = 0; c < PF; ++c) {
-    wv[c] = ld_tile < ntiles ? *(const uint4*)(ld_p + ld_c * CH) : uint4{0, 0, 0, 0};
+  auto load_next = [&]() {
+    const uint4 v = *(const uint4*)(ld_p + ld_c * CH);
     if (++ld_c == nch) {
       ld_c = 0;
       ld_tile += stride;
       ld_p = row_ptr(ld_tile);
     }
-  }
+    return v;
+  };
+  uint4 wa[PF], wb[PF];
+#pragma unroll
+  for (int c = 0; c < PF; ++c) wa[c] = load_next();
   // Stage the (up to 64) rows while the first weight chunks are in flight: 16-row tiles, each
   // with the RMSNorm prologue.
   for (int mt = 0; mt < MT; ++mt) {
@@ -535,22 +542,37 @@ __global__ __launch_bounds__(64 * W) void lm_head_argmax_kernel(RowsArgs a) {
     f32x4 acc[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int c0 = 0; c0 < nch; c0 += PF) {
-#pragma unroll
-      for (int c = 0; c < PF; ++c) {
-        const uint4 cur = wv[c];
-        if (ld_tile < ntiles) wv[c] = *(const uint4*)(ld_p + ld_c * CH);  // wave-uniform
-        if (++ld_c == nch) {
-          ld_c = 0;
-          ld_tile += stride;
-          ld_p = row_ptr(ld_tile);
-        }
+    if constexpr (PF == 1) {  // any chunk count: one slot, copied (the slow path)
+      for (int c = 0; c < nch; ++c) {
+        const uint4 cur = wa[0];
+        wa[0] = load_next();
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-          const bf16x8 av = *(const bf16x8*)(smem + (mt * 16 + j) * ldsx + (c0 + c) * CH + g * 8);
+          const bf16x8 av = *(const bf16x8*)(smem + (mt * 16 + j) * ldsx + c * CH + g * 8);
           acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8, cur), acc[mt], 0, 0, 0);
         }
       }
+    } else {
+    for (int c0 = 0; c0 < nch; c0 += 2 * PF) {  // nch is a multiple of 2 * PF (the host checks)
+#pragma unroll
+      for (int c = 0; c < PF; ++c) {
+        wb[c] = load_next();
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const bf16x8 av = *(const bf16x8*)(smem + (mt * 16 + j) * ldsx + (c0 + c) * CH + g * 8);
+          acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8, wa[c]), acc[mt], 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < PF; ++c) {
+        wa[c] = load_next();
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const bf16x8 av = *(const bf16x8*)(smem + (mt * 16 + j) * ldsx + (c0 + PF + c) * CH + g * 8);
+          acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8, wb[c]), acc[mt], 0, 0, 0);
+        }
+      }
+    }
     }
     // lane (g, j) holds logits of tokens mt*16 + 4g + i for vocabulary row `row`
 #pragma unroll
@@ -881,8 +903,8 @@ extern "C" int msa_lm_head_argmax(const uint16_t* hidden, int64_t ld_hidden, int
   rc = norm_w ? launch_rows(lm_head_argmax_kernel<W, MT, RB_PRO_GATHER_RMSNORM, PF>, 64 * W, lds, kLmBlocks, a, s) \
               : launch_rows(lm_head_argmax_kernel<W, MT, RB_PRO_GATHER, PF>, 64 * W, lds, kLmBlocks, a, s)
 #define MSA_LM_LAUNCH(MT)                                  \
-  if (nch % 16 == 0) MSA_LM_LAUNCH_PF(MT, 16);             \
-  else if (nch % 4 == 0) MSA_LM_LAUNCH_PF(MT, 4);          \
+  if (nch % 32 == 0) MSA_LM_LAUNCH_PF(MT, 16);             \
+  else if (nch % 8 == 0) MSA_LM_LAUNCH_PF(MT, 4);          \
   else MSA_LM_LAUNCH_PF(MT, 1);
     switch (mt) {
       case 1: MSA_LM_LAUNCH(1); break;
