@@ -696,14 +696,22 @@ constexpr int kDecodeW = 4;  // wavefronts per decode workgroup
 // Keys per workgroup-level split: at most 64 blocks per wavefront (one table entry per lane).
 constexpr int kDecodeMaxPartTokens = 64 * kDecodeW * kBlock;
 
+// The plain entry point takes eight wavefronts per workgroup for splits of at least this many
+// keys: each wavefront then streams fewer blocks of a long context (64 sequences at contexts
+// U[128, 2048]: 5.2 against 4.0 TB/s) when G <= 2 (with G = 4, 207 VGPRs, an eight-wavefront
+// workgroup fills a CU alone: slower). Shorter splits, and the fused decode-step entry point
+// always, take four: their workgroups of a decode batch are all resident at once (three share a
+// CU at the kernel's register count for G <= 2), and the fused step's result must not depend on
+// the split size its caller derives from a padded block table.
+constexpr int kDecodeWideTokens = 1024;
+
 template <int G, bool QKV = false>
 static void launch_decode(const DecodeArgs& a, int num_seqs, hipStream_t s) {
-  // Four wavefronts per workgroup: at the kernel's register count (three wavefronts per SIMD for
-  // G <= 2) three workgroups share a CU, so a batch's (sequence, KV head) pairs are resident at
-  // once.
-  constexpr int W = kDecodeW;
   const dim3 grid(a.kv_heads, a.splits, num_seqs);
-  hipLaunchKernelGGL((paged_decode_kernel<G, W, QKV>), grid, dim3(64 * W), 0, s, a);
+  if (!QKV && G <= 2 && a.part_tokens >= kDecodeWideTokens)
+    hipLaunchKernelGGL((paged_decode_kernel<G, 2 * kDecodeW, QKV>), grid, dim3(128 * kDecodeW), 0, s, a);
+  else
+    hipLaunchKernelGGL((paged_decode_kernel<G, kDecodeW, QKV>), grid, dim3(64 * kDecodeW), 0, s, a);
 }
 
 // Shared checks and workspace binding of the two decode entry points.
