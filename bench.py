@@ -46,6 +46,9 @@ BATCH, CTX_LO, CTX_HI = 64, 256, 384
 # from rocprofv3 --pmc: 42,902.07 KiB x 2 x 1024 + 512 KiB x 1024
 # (profiles/paged_decode_kernel_traffic_pmc.md).
 ATTN_TRAFFIC_BYTES: int | None = 88_321_135
+# The same counters over one layer's four decode linears (profiles/dec_linear_kernel_pmc.md); None
+# until measured.
+LINEAR_TRAFFIC_BYTES: int | None = None
 
 
 def log(msg: str) -> None:
@@ -53,7 +56,28 @@ def log(msg: str) -> None:
 
 
 def cpu_threads() -> int:
-    return min(len(os.sched_getaffinity(0)), 16)
+    """Every core this process may run on (its CPU affinity)."""
+    return len(os.sched_getaffinity(0))
+
+
+def cpu_model() -> str:
+    """The host CPU's model name as ``lscpu`` prints it."""
+    import subprocess
+
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10, check=True).stdout
+        for ln in out.splitlines():
+            if ln.strip().startswith("Model name:"):
+                return ln.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        for ln in Path("/proc/cpuinfo").read_text().splitlines():
+            if ln.startswith("model name"):
+                return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
 
 def hip_time(launch, count: int, reps: int = 3) -> float:
@@ -78,12 +102,14 @@ def hip_time(launch, count: int, reps: int = 3) -> float:
     return best
 
 
-def cpu_time(fn, budget_s: float = 20.0, max_reps: int = 5) -> tuple[float, int]:
-    """Median seconds of ``fn()`` on the host after one warm-up, as many runs as fit the budget."""
+def cpu_time(fn, budget_s: float = 20.0, max_reps: int = 5, min_reps: int = 5) -> tuple[float, int]:
+    """Median seconds of ``fn()`` on the host after two warm-ups, at least ``min_reps`` runs and as
+    many more (up to ``max_reps``) as fit the budget."""
+    fn()
     t = time.perf_counter()
     fn()
     first = time.perf_counter() - t
-    reps = max(1, min(max_reps, int(budget_s / max(first, 1e-6))))
+    reps = max(min_reps, min(max_reps, int(budget_s / max(first, 1e-6))))
     times = []
     for _ in range(reps):
         t = time.perf_counter()
@@ -96,8 +122,8 @@ def cpu_time(fn, budget_s: float = 20.0, max_reps: int = 5) -> tuple[float, int]
 def cpu_fields(value: float, unit: str, sample: str) -> dict:
     import torch
 
-    return {"value": round(value, 3), "unit": unit, "cores": cpu_threads(), "kind": "port", "sample": sample,
-            "cpu": platform.processor() or platform.machine(), "torch": torch.__version__}
+    return {"value": round(value, 3), "unit": unit, "cores": torch.get_num_threads(), "kind": "port", "sample": sample,
+            "cpu": cpu_model(), "torch": torch.__version__}
 
 
 def roofline(kernel: str, bound: str, achieved: float, per_launch: int, secs: float, traffic=None) -> dict:
@@ -218,6 +244,87 @@ def time_layer_attention(runner, sched, cfg, fused: bool = True) -> tuple[float,
     return secs, attention_qkv_bytes(ctx, heads, kvh, dim), f"paged_decode_kernel<{heads // kvh}, 4, true>"
 
 
+def decode_linear_bytes(m: int, n: int, k: int, epilogue: int, norm: bool) -> int:
+    """One decode-step linear as it runs in the step: int8 weights, bf16 row scales, bf16 x in, bf16 y
+    out (n / 2 columns after silu * up), plus the residual read of a residual epilogue and the
+    RMSNorm weights of a norm prologue."""
+    from miniserve_amd import kernels
+
+    cols = n // 2 if epilogue == kernels.EPI_SILU_MUL else n
+    extra = (2 * m * n if epilogue == kernels.EPI_RESIDUAL else 0) + (2 * k if norm else 0)
+    return n * k + 2 * n + 2 * m * k + 2 * m * cols + extra
+
+
+def time_layer_linears(model, tokens: int, dev) -> list[tuple[str, float, int]]:
+    """The four int8 decode linears of a layer as the decode step runs them (the decode-linear kernel
+    with the step's prologues and epilogues, ``tokens`` activation rows), each timed over one launch
+    per layer on that layer's own weights (28 x 18 MB, more than the Infinity Cache holds); returns
+    (name, seconds per launch, algorithmic bytes per launch) per linear."""
+    import torch
+
+    from miniserve_amd import kernels
+
+    cfg = model.cfg
+    h, qsz, inter = cfg.hidden_size, cfg.num_attention_heads * cfg.head_dim, cfg.intermediate_size
+    g = torch.Generator(device=dev).manual_seed(11)
+    x = torch.randn(tokens, h, generator=g, device=dev).to(torch.bfloat16)
+    a = torch.randn(tokens, qsz, generator=g, device=dev).to(torch.bfloat16)
+    act = torch.randn(tokens, inter, generator=g, device=dev).to(torch.bfloat16)
+    res = torch.randn(tokens, h, generator=g, device=dev).to(torch.bfloat16)
+    layers = model.layers
+    out = []
+
+    def qkv(i):
+        ly = layers[i]
+        kernels.int8_linear_dec(x, ly.self_attn.qkv_proj.qweight, ly.self_attn.qkv_proj.kscale,
+                                norm_w=ly.input_layernorm.weight, eps=cfg.rms_norm_eps)
+
+    def o(i):
+        p = layers[i].self_attn.o_proj
+        kernels.int8_linear_dec(a, p.qweight, p.kscale, kernels.EPI_RESIDUAL, residual=res, out=res)
+
+    def gate_up(i):
+        ly = layers[i]
+        kernels.int8_linear_dec(x, ly.mlp.gate_up_proj.qweight, ly.mlp.gate_up_proj.kscale, kernels.EPI_SILU_MUL,
+                                norm_w=ly.post_attention_layernorm.weight, eps=cfg.rms_norm_eps)
+
+    def down(i):
+        p = layers[i].mlp.down_proj
+        kernels.int8_linear_dec(act, p.qweight, p.kscale, kernels.EPI_RESIDUAL, residual=res, out=res)
+
+    for name, fn, n, k, epi, norm in (
+        ("qkv + input RMSNorm", qkv, qsz + 2 * cfg.num_key_value_heads * cfg.head_dim, h, kernels.EPI_NONE, True),
+        ("o + residual", o, h, qsz, kernels.EPI_RESIDUAL, False),
+        ("gate_up + RMSNorm + silu*up", gate_up, 2 * inter, h, kernels.EPI_SILU_MUL, True),
+        ("down + residual", down, h, inter, kernels.EPI_RESIDUAL, False),
+    ):
+        secs = hip_time(fn, len(layers), reps=4)
+        out.append((name, secs, decode_linear_bytes(tokens, n, k, epi, norm)))
+    return out
+
+
+def copy_bandwidth(dev) -> float:
+    """GB/s of a 512 MiB device copy counted as 2x its bytes, the median of 5 runs of 20 copies
+    after 3 warm-up copies (the reference's measurement, bench/bandwidth.py:21-34)."""
+    import torch
+
+    x = torch.empty(256 << 20, dtype=torch.bfloat16, device=dev)
+    y = torch.empty_like(x)
+    runs = []
+    for _ in range(5):
+        for _ in range(3):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        for _ in range(20):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        runs.append(2 * x.numel() * 2 * 20 / (time.perf_counter() - t) / 1e9)
+    del x, y
+    torch.cuda.empty_cache()
+    return sorted(runs)[2]
+
+
 def time_graph_steps(runner, sched, steps: int, warmup: int) -> float:
     import torch
 
@@ -277,6 +384,22 @@ def bench_decode(args) -> dict:
         "kv_block": 16, "weights": "int8 per-output-channel, bf16 activations, fp32 accumulation, tied bf16 LM head",
         "parallelism": "none", "hip_graph": True, "eager_ms_per_step": round(eager_dt * 1e3, 4)})
     out["roofline"] = roofline(kname, "hbm", nbytes / secs / 1e9, nbytes, secs, ATTN_TRAFFIC_BYTES)
+    # The other half of the metric: the four int8 decode linears of a layer, their algorithmic bytes
+    # over their summed kernel time.
+    lins = time_layer_linears(model, BATCH, dev)
+    lin_secs, lin_bytes = sum(t for _, t, _ in lins), sum(b for _, _, b in lins)
+    for name, t, b in lins:
+        log(f"decode linear {name}: {t * 1e6:.2f} us/launch, {b / t / 1e9:.0f} GB/s")
+    out["roofline_gemv"] = roofline("dec_linear_kernel (qkv, o, gate_up, down of one layer)", "hbm",
+                                    lin_bytes / lin_secs / 1e9, lin_bytes, lin_secs)
+    out["roofline_gemv"]["per_linear_us"] = {name: round(t * 1e6, 3) for name, t, _ in lins}
+    out["roofline_gemv"]["traffic"] = LINEAR_TRAFFIC_BYTES
+    copy = copy_bandwidth(dev)
+    log(f"copy bandwidth (512 MiB, 2x bytes): {copy:.0f} GB/s")
+    out["copy_bandwidth"] = {"value": round(copy, 1), "unit": "GB/s", "frac_of_peak": round(copy / HBM_PEAK_GBS, 4),
+                             "method": "512 MiB device copy x 20, 2x bytes, median of 5"}
+    for key in ("roofline", "roofline_gemv"):
+        out[key]["frac_of_copy_bw"] = round(out[key]["achieved"] / copy, 4)
     if not args.no_cpu_baseline:
         from oracle import model as om
 
@@ -289,7 +412,7 @@ def bench_decode(args) -> dict:
         med, reps = cpu_time(lambda: om.run_step(ocfg, ow, okv, step, 16, tables))
         log(f"cpu oracle: {med:.3f} s/step on {cpu_threads()} threads")
         out["cpu_baseline"] = cpu_fields(BATCH / med, "tok/s", "the full decode step (64 tokens, 28 layers, LM head, "
-                                         f"argmax), median of {reps} after 1 warm-up")
+                                         f"argmax), median of {reps} after 2 warm-ups")
     return out
 
 

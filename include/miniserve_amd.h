@@ -101,11 +101,9 @@ int msa_int8_linear_rows(const uint16_t* x, int64_t ldx, int64_t m, int64_t k, c
  * are x[gather_rows[t]] (indices clamped into [0, x_rows); the embedding lookup of
  * model/qwen3.py:148, then also copied to x_copy: the residual stream) when gather_rows is
  * non-NULL, else x[t]. norm_w non-NULL applies RMSNorm(x) first (model/layers.py:18-22 with eps;
- * the input_layernorm / post_attention_layernorm of model/qwen3.py:121-122). The int8 weights
- * enter the products exactly and the row scale and the norm's row factor multiply the float32
- * dot products (y = r * s * sum(bf16(x * w) * q)), not bf16(q * s) and bf16(w * bf16(x * r))
- * element by element as in the reference: rel-L2 ~4e-3 from the reference's rounding, closer to
- * the float64 value. Epilogues as msa_int8_linear (MSA_EPI_RESIDUAL may write y in place over
+ * the input_layernorm / post_attention_layernorm of model/qwen3.py:121-122). Rounded where the
+ * reference rounds: weights dequantized to bf16(q * s), the norm as bf16(w * bf16(x * r)),
+ * float32 accumulation, bf16 output. Epilogues as msa_int8_linear (MSA_EPI_RESIDUAL may write y in place over
  * residual); gather_rows takes MSA_EPI_NONE and needs norm_w. k in {1024, 2048, 3072, 4096}; x,
  * qweight, norm_w, x_copy 16-byte aligned with row strides % 8 == 0. */
 int msa_int8_linear_dec(const uint16_t* x, int64_t ldx, int64_t x_rows, const int64_t* gather_rows,

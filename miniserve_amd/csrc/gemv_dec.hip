@@ -11,20 +11,20 @@
 //     (the A operand of v_mfma_f32_16x16x32_bf16: token row j, 16 consecutive K values per chunk),
 //     the norm weights, its int8 weight fragments (B operand: weight row j, 16 bytes per chunk),
 //     the row scales and the residual values its epilogue will add.
-//  2. RMSNorm prologue (model/layers.py:18-22): each wavefront sums the squares of its K slice on
-//     bf16 pairs (v_dot2_f32_bf16), the KW partial sums of each token meet in LDS (one barrier),
-//     and each lane multiplies its own fragments by the norm weight, bf16(x * w). The row factor
-//     rsqrt(mean(x^2) + eps) is linear in the product and is applied in the epilogue.
-//  3. Each 16-byte weight fragment is converted once to bf16 -- exactly: |q| <= 127 -- and feeds
-//     the MT token tiles. The per-row scale (quant/int8.py:36) is likewise applied in the epilogue,
-//     to the float32 dot product: y = r * s * sum(x * w * q). The reference instead rounds
-//     bf16(q * s) and bf16(w * bf16(x * r)) element by element before its bf16 product; the two
-//     differ by those roundings (rel-L2 ~4e-3), and this form is the closer of the two to the
-//     float64 value of the same int8 weights (~2e-3 against ~3e-3).
+//  2. RMSNorm prologue (model/layers.py:18-22), rounded as the reference rounds it: each wavefront
+//     sums the squares of its K slice on bf16 pairs (v_dot2_f32_bf16, exact products), the KW
+//     partial sums of each token meet in LDS (one barrier), and each lane turns its fragments into
+//     bf16(w * bf16(x * r)) with r = rsqrt(mean(x^2) + eps) -- x * r rounded by one packed
+//     conversion, the weight product taken exactly on v_dot2_f32_bf16 against the weight with its
+//     other half zeroed, then rounded again.
+//  3. Each 16-byte weight fragment is dequantized once to bf16(q * s) -- the value of the
+//     reference's whole-matrix dequantization (quant/int8.py:36) -- and feeds the MT token tiles
+//     (v_mfma_f32_16x16x32_bf16, float32 accumulation): the same operands, rounded at the same
+//     points, as the reference's bf16 product.
 //  4. The KW partial accumulators meet in LDS (second barrier); the output tiles are spread over
 //     the wavefronts, each summing the KW partials in a fixed order (deterministic) and applying
-//     r * s and the epilogue: plain bf16 store, residual add (model/qwen3.py:121-122) or
-//     silu(gate) * up with the gate and up tiles in the same workgroup (model/layers.py:77-78).
+//     the epilogue: plain bf16 store, residual add (model/qwen3.py:121-122) or silu(gate) * up
+//     with the gate and up tiles in the same workgroup (model/layers.py:77-78).
 //
 // The K mapping inside a 64-wide chunk is permuted identically for A and B (lane group g takes K
 // offsets [16g, 16g + 16) and splits them over the two MFMA k-steps), which leaves the dot
@@ -65,10 +65,11 @@ struct DecLinArgs {
 };
 
 
-// bf16(x * w) on a pair of bf16: the RMSNorm weight applied to the activations; the row factor
-// rsqrt(mean(x^2) + eps) is applied to the finished dot products.
-__device__ __forceinline__ uint32_t weight_pair(uint32_t xv, uint32_t wv) {
-  return pack_bf16x2(bf16lo(xv) * bf16lo(wv), bf16hi(xv) * bf16hi(wv));
+// RMSNorm of a bf16 pair as model/layers.py:18-22 rounds it: bf16(w * bf16(x * r)). wlo / whi are
+// the norm weight pair with the other half zeroed, so v_dot2_f32_bf16 gives each product exactly.
+__device__ __forceinline__ uint32_t norm_pair(uint32_t xv, uint32_t wlo, uint32_t whi, float r) {
+  const uint32_t xr = pack_bf16x2(bf16lo(xv) * r, bf16hi(xv) * r);
+  return pack_bf16x2(dot2_bf16(xr, wlo, 0.f), dot2_bf16(xr, whi, 0.f));
 }
 
 // Weight row of tile nt, lane row j. SILU_MUL: tiles [0, NT/2) are gate rows, [NT/2, NT) the
@@ -228,20 +229,37 @@ __global__ __launch_bounds__(64 * KW) __attribute__((amdgpu_waves_per_eu(1, 1)))
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) s_ss[ks][mt * 16 + j] = ss[mt];
     }
+    __syncthreads();  // every wavefront's partial sums of squares
+    // This lane's A-fragment rows are tokens mt * 16 + j.
+    float rn[MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+    for (int mt = 0; mt < MT; ++mt) {
+      float tot = 0.f;
 #pragma unroll
-      for (int c = 0; c < CH; ++c)
+      for (int w = 0; w < KW; ++w) tot += s_ss[w][mt * 16 + j];
+      rn[mt] = 1.0f / sqrtf(tot / (float)a.k + a.eps);
+    }
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+    for (int c = 0; c < CH; ++c)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint4 wn = nw[c][h];
+        const uint32_t wl[4] = {wn.x & 0xffffu, wn.y & 0xffffu, wn.z & 0xffffu, wn.w & 0xffffu};
+        const uint32_t wh[4] = {wn.x & 0xffff0000u, wn.y & 0xffff0000u, wn.z & 0xffff0000u, wn.w & 0xffff0000u};
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
           uint4& v = xa[mt][c][h];
-          const uint4 wn = nw[c][h];
-          v = uint4{weight_pair(v.x, wn.x), weight_pair(v.y, wn.y), weight_pair(v.z, wn.z), weight_pair(v.w, wn.w)};
+          const float r = rn[mt];
+          v = uint4{norm_pair(v.x, wl[0], wh[0], r), norm_pair(v.y, wl[1], wh[1], r),
+                    norm_pair(v.z, wl[2], wh[2], r), norm_pair(v.w, wl[3], wh[3], r)};
         }
-    __syncthreads();  // the row sums of squares are read by the epilogue
+      }
   }
 
-  // ---- 3. int8 weights as exact bf16, MFMA over the MT token tiles (scales applied after) ----
+  // ---- 3. int8 weights dequantized to bf16(q * s), MFMA over the MT token tiles ----
+  float sf[NT];  // this lane's weight row scale in each tile (lane row j)
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) sf[nt] = bf16_to_f32(scb[nt]);
   f32x4 acc[MT][NT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
@@ -253,7 +271,7 @@ __global__ __launch_bounds__(64 * KW) __attribute__((amdgpu_waves_per_eu(1, 1)))
     for (int h = 0; h < 2; ++h)
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
-        const bf16x8 bv = h == 0 ? int8x8_to_bf16(wv[nt][c].x, wv[nt][c].y) : int8x8_to_bf16(wv[nt][c].z, wv[nt][c].w);
+        const bf16x8 bv = h == 0 ? dequant8(wv[nt][c].x, wv[nt][c].y, sf[nt]) : dequant8(wv[nt][c].z, wv[nt][c].w, sf[nt]);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
           acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xa[mt][c][h]), bv,
@@ -289,36 +307,18 @@ __global__ __launch_bounds__(64 * KW) __attribute__((amdgpu_waves_per_eu(1, 1)))
     const int col = SILU ? (rb * NP + np) * 16 + j : dec_row<NT, EPI>(a, rb, np, j);
     const int ncols = SILU ? a.n / 2 : a.n;
     if (col >= ncols) continue;
-    // this lane's column scale(s) (weight row j of tile np / np + NP) and row factors
-    uint32_t sb0 = 0, sb1 = 0;  // selected with constant indices (np varies by wavefront)
-#pragma unroll
-    for (int nt = 0; nt < NP; ++nt) {
-      sb0 = nt == np ? scb[nt] : sb0;
-      if constexpr (SILU) sb1 = nt == np ? scb[nt + NP] : sb1;
-    }
-    const float s0 = bf16_to_f32(sb0), s1 = bf16_to_f32(sb1);
-    float rf[4] = {1.f, 1.f, 1.f, 1.f};
-    if constexpr (NORM) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float tot = 0.f;
-#pragma unroll
-        for (int w = 0; w < KW; ++w) tot += s_ss[w][mt * 16 + 4 * g + i];
-        rf[i] = 1.0f / sqrtf(tot / (float)a.k + a.eps);
-      }
-    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int tl = tbase + mt * 16 + 4 * g + i;
       if (tl >= a.t) continue;
       float o;
       if constexpr (SILU) {
-        const float gt = round_bf16(v0[i] * (rf[i] * s0)), up = round_bf16(v1[i] * (rf[i] * s1));
+        const float gt = round_bf16(v0[i]), up = round_bf16(v1[i]);
         o = round_bf16(silu_f32(gt)) * up;
       } else if constexpr (EPI == DL_EPI_RESIDUAL) {
-        o = round_bf16(v0[i] * (rf[i] * s0)) + bf16_to_f32(rres[uu][i]);
+        o = round_bf16(v0[i]) + bf16_to_f32(rres[uu][i]);
       } else {
-        o = v0[i] * (rf[i] * s0);
+        o = v0[i];
       }
       a.y[(int64_t)tl * a.ldy + col] = f32_to_bf16(o);
     }

@@ -722,9 +722,15 @@ def verify_sampled(
         _check(tuple(draft_probs.shape) == (b, k, v), "verify_sampled: draft_probs [B, K, V]")
         dp = draft_probs.float().contiguous()
     _check(tuple(uniform.shape) == (b, k) and tuple(noise.shape) == (b, v), "verify_sampled: uniform [B, K], noise [B, V]")
+    # Every converted operand is held by a local until the launch is queued: a temporary passed
+    # straight to _ptr would return its memory to the caching allocator first, and the next
+    # conversion could be given (and overwrite) that block before the kernel reads it.
+    dr = _i64(drafts, (b, k), "drafts")
+    nd = _i64(num_drafts, (b,), "num_drafts")
+    un = uniform.float().contiguous()
+    nz = noise.float().contiguous()
     accepted = torch.empty(b, dtype=torch.int64, device=tp.device)
     nxt = torch.empty_like(accepted)
-    _native.call("msa_verify_sampled", _ptr(tp), b, k, v, _ptr(_i64(drafts, (b, k), "drafts")),
-                 _ptr(_i64(num_drafts, (b,), "num_drafts")), _ptr(dp), _ptr(uniform.float().contiguous()),
-                 _ptr(noise.float().contiguous()), _ptr(accepted), _ptr(nxt), _stream(tp))
+    _native.call("msa_verify_sampled", _ptr(tp), b, k, v, _ptr(dr), _ptr(nd), _ptr(dp), _ptr(un), _ptr(nz),
+                 _ptr(accepted), _ptr(nxt), _stream(tp))
     return accepted, nxt

@@ -1,9 +1,9 @@
 """The building blocks of a Qwen3 layer (reference: src/miniserve/model/layers.py).
 
-RMSNorm runs as a HIP kernel; RoPE is applied inside the fused q/k-norm + RoPE + KV-write kernel
-of ``Qwen3Attention`` (``rotate_half`` / ``apply_rope`` are kept with the reference's semantics for
-callers that use them directly); SwiGLU with int8 projections runs silu(gate) * up in the epilogue
-of the gate_up kernel and the residual add in the epilogue of the down kernel.
+RMSNorm runs as a HIP kernel; RoPE is applied inside the fused q/k-norm + RoPE + KV-write kernels
+of ``Qwen3Attention`` from the float32 tables built here; SwiGLU with int8 projections runs
+silu(gate) * up in the epilogue of the gate_up kernel and the residual add in the epilogue of the
+down kernel.
 """
 
 from __future__ import annotations
@@ -56,18 +56,6 @@ class RotaryEmbedding(nn.Module):
 
     def forward(self, positions: Tensor) -> tuple[Tensor, Tensor]:
         return self.cos[positions], self.sin[positions]
-
-
-def rotate_half(x: Tensor) -> Tensor:
-    x1, x2 = x.chunk(2, dim=-1)
-    return torch.cat((-x2, x1), dim=-1)
-
-
-def apply_rope(q: Tensor, k: Tensor, cos: Tensor, sin: Tensor) -> tuple[Tensor, Tensor]:
-    """q: [T, heads, head_dim], k: [T, kv_heads, head_dim], cos/sin: [T, head_dim] (layers.py:61-65)."""
-    cos = cos.unsqueeze(1).to(q.dtype)
-    sin = sin.unsqueeze(1).to(q.dtype)
-    return q * cos + rotate_half(q) * sin, k * cos + rotate_half(k) * sin
 
 
 class SwiGLU(nn.Module):

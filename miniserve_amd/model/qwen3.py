@@ -144,6 +144,11 @@ class Qwen3ForCausalLM(nn.Module):
         self.lm_head: nn.Linear | None = (
             None if cfg.tie_word_embeddings else nn.Linear(cfg.hidden_size, cfg.vocab_size, bias=False)
         )
+        # Token-split batches of up to DEC_MAX_TOKENS tokens run their linears on the decode kernel
+        # (row scale and norm factor applied to the float32 dot products); False keeps them on the
+        # rows kernel, which rounds bf16(q * s) and the normed activations per element as the
+        # reference does (a slower path, kept to compare the two roundings).
+        self.decode_linears = True
 
     def forward(
         self,
@@ -215,91 +220,117 @@ class Qwen3ForCausalLM(nn.Module):
     def _token_split_layers(
         self, input_ids: Tensor, positions: Tensor, kv_caches: list[tuple[Tensor, Tensor]], meta: AttentionMetadata
     ) -> Tensor:
-        """The layer loop on the token-split kernels, four launches plus attention per layer:
-          [embedding gather (layer 0) + input RMSNorm + int8 qkv + q/k-norm + RoPE + KV write]
-          -> paged attention -> [int8 o + residual add]
-          -> [post-attention RMSNorm + int8 gate_up + silu * up] -> [int8 down + residual add]
-        Returns the residual stream after the last layer (before the final norm)."""
-        cfg = self.cfg
+        """The layer loop on the token-split kernels (``token_split_layer`` per layer). Returns the
+        residual stream after the last layer (before the final norm)."""
         t = input_ids.numel()
         ids = input_ids if input_ids.dtype == torch.int64 and input_ids.is_contiguous() else input_ids.long().contiguous()
         pos = positions if positions.dtype == torch.int64 and positions.is_contiguous() else positions.long().contiguous()
-        residual = torch.empty(t, cfg.hidden_size, dtype=torch.bfloat16, device=ids.device)
+        residual = torch.empty(t, self.cfg.hidden_size, dtype=torch.bfloat16, device=ids.device)
+        for i, (k_cache, v_cache) in enumerate(kv_caches):
+            self.token_split_layer(i, residual, k_cache, v_cache, meta, pos, ids if i == 0 else None)
+        return residual
+
+    def token_split_layer(
+        self,
+        i: int,
+        residual: Tensor,
+        k_cache: Tensor,
+        v_cache: Tensor,
+        meta: AttentionMetadata,
+        positions: Tensor,
+        input_ids: Tensor | None = None,
+    ) -> None:
+        """Decoder layer ``i`` (model/qwen3.py:112-122) on the token-split kernels, four launches plus
+        attention, updating the residual stream [T, hidden] in place:
+          [embedding gather (``input_ids``, layer 0) + input RMSNorm + int8 qkv (+ q/k-norm + RoPE +
+          KV write)] -> paged attention -> [int8 o + residual add]
+          -> [post-attention RMSNorm + int8 gate_up + silu * up] -> [int8 down + residual add]
+        A pure-decode batch of up to DEC_MAX_TOKENS tokens runs the qkv projection as a plain decode
+        linear and the per-head norms, RoPE and KV write inside the decode attention kernel."""
+        cfg = self.cfg
+        t = residual.shape[0]
         rot = self.rotary
+        layer = self.layers[i]
+        attn, mlp = layer.self_attn, layer.mlp
+        qkv, o, gu, dn = attn.qkv_proj, attn.o_proj, mlp.gate_up_proj, mlp.down_proj
 
         def lin(k: int):
             # Up to DEC_MAX_TOKENS tokens the decode kernel (activations straight into MFMA
             # operands, all loads in flight at once) serves the K it supports; else the
             # token-split rows kernel.
-            if t <= kernels.DEC_MAX_TOKENS and kernels.dec_supported(k):
+            if t <= kernels.DEC_MAX_TOKENS and kernels.dec_supported(k) and self.decode_linears:
                 return kernels.int8_linear_dec
             return kernels.int8_linear_rows
 
-        # Pure-decode batches: the qkv projection as a plain decode linear and the per-head norms,
-        # RoPE and KV write inside the decode attention kernel.
         fused_decode = (
             meta.prefill is None and meta.decode is not None and t <= kernels.DEC_MAX_TOKENS
-            and kernels.dec_supported(cfg.hidden_size)
+            and kernels.dec_supported(cfg.hidden_size) and self.decode_linears
         )
-        for i, (layer, (k_cache, v_cache)) in enumerate(zip(self.layers, kv_caches, strict=True)):
-            attn, mlp = layer.self_attn, layer.mlp
-            qkv, o, gu, dn = attn.qkv_proj, attn.o_proj, mlp.gate_up_proj, mlp.down_proj
-            first = i == 0
-            src = self.embed_tokens.weight if first else residual
-            if fused_decode:
-                # [gather + input RMSNorm + int8 qkv] -> [q/k-norm + RoPE + KV write + attention]
-                qkv_rows = kernels.int8_linear_dec(
-                    src, qkv.qweight, qkv.scale, norm_w=layer.input_layernorm.weight, eps=layer.input_layernorm.eps,
-                    gather=ids if first else None, x_copy=residual if first else None,
-                )
-                a = attend_decode_qkv(
-                    qkv_rows, attn.num_heads, attn.q_norm.weight, attn.k_norm.weight, attn.q_norm.eps, rot.cos,
-                    rot.sin, k_cache, v_cache, meta, attn.scale,
-                ).view(t, attn.q_size)
-            else:
-                q = kernels.qkv_rope_cache_rows(
-                    src, qkv.qweight, qkv.scale, attn.num_heads, attn.num_kv_heads, attn.head_dim,
-                    attn.q_norm.weight, attn.k_norm.weight, attn.q_norm.eps, pos, rot.cos, rot.sin,
-                    meta.slot_mapping, k_cache, v_cache, norm_w=layer.input_layernorm.weight,
-                    eps=layer.input_layernorm.eps, gather=ids if first else None, x_copy=residual if first else None,
-                )
-                a = attend(q, k_cache, v_cache, meta, attn.scale).view(t, attn.q_size)
-            lin(attn.q_size)(a, o.qweight, o.scale, kernels.EPI_RESIDUAL, residual=residual, out=residual)
-            act = lin(cfg.hidden_size)(
-                residual, gu.qweight, gu.scale, kernels.EPI_SILU_MUL,
-                norm_w=layer.post_attention_layernorm.weight, eps=layer.post_attention_layernorm.eps,
+        first = input_ids is not None
+        src = self.embed_tokens.weight if first else residual
+        if fused_decode:
+            # [gather + input RMSNorm + int8 qkv] -> [q/k-norm + RoPE + KV write + attention]
+            qkv_rows = kernels.int8_linear_dec(
+                src, qkv.qweight, qkv.kscale, norm_w=layer.input_layernorm.weight, eps=layer.input_layernorm.eps,
+                gather=input_ids, x_copy=residual if first else None,
             )
-            lin(cfg.intermediate_size)(act, dn.qweight, dn.scale, kernels.EPI_RESIDUAL, residual=residual, out=residual)
-        return residual
+            a = attend_decode_qkv(
+                qkv_rows, attn.num_heads, attn.q_norm.weight, attn.k_norm.weight, attn.q_norm.eps, rot.cos,
+                rot.sin, k_cache, v_cache, meta, attn.scale,
+            ).view(t, attn.q_size)
+        else:
+            q = kernels.qkv_rope_cache_rows(
+                src, qkv.qweight, qkv.kscale, attn.num_heads, attn.num_kv_heads, attn.head_dim,
+                attn.q_norm.weight, attn.k_norm.weight, attn.q_norm.eps, positions, rot.cos, rot.sin,
+                meta.slot_mapping, k_cache, v_cache, norm_w=layer.input_layernorm.weight,
+                eps=layer.input_layernorm.eps, gather=input_ids, x_copy=residual if first else None,
+            )
+            a = attend(q, k_cache, v_cache, meta, attn.scale).view(t, attn.q_size)
+        lin(attn.q_size)(a, o.qweight, o.kscale, kernels.EPI_RESIDUAL, residual=residual, out=residual)
+        act = lin(cfg.hidden_size)(
+            residual, gu.qweight, gu.kscale, kernels.EPI_SILU_MUL,
+            norm_w=layer.post_attention_layernorm.weight, eps=layer.post_attention_layernorm.eps,
+        )
+        lin(cfg.intermediate_size)(act, dn.qweight, dn.kscale, kernels.EPI_RESIDUAL, residual=residual, out=residual)
 
     def _fused_forward(
         self, x: Tensor, cos: Tensor, sin: Tensor, kv_caches: list[tuple[Tensor, Tensor]], meta: AttentionMetadata
     ) -> Tensor:
-        """The layer loop for batches above the token-split limit (prefill chunks): int8 linears on
-        the LDS-tiled MFMA GEMM (silu * up in its epilogue; the o and down projections add the
-        residual and apply the next RMSNorm, merging split-K partials in the same pass), the first
-        RMSNorm and the q/k-norm + RoPE + KV-write as their own kernels. Returns norm(x_L), the same
-        value as the module-by-module loop; ``x`` (the embedding output) is updated in place as the
-        residual stream."""
+        """The layer loop for batches above the token-split limit (prefill chunks), ``gemm_layer``
+        per layer. Returns norm(x_L), the same value as the module-by-module loop; ``x`` (the
+        embedding output) is updated in place as the residual stream."""
+        layers = self.layers
+        h = kernels.rmsnorm(x, layers[0].input_layernorm.weight, layers[0].input_layernorm.eps)
+        for i, (k_cache, v_cache) in enumerate(kv_caches):
+            h = self.gemm_layer(i, x, h, cos, sin, k_cache, v_cache, meta)
+        return h
+
+    def gemm_layer(
+        self, i: int, x: Tensor, h: Tensor, cos: Tensor, sin: Tensor, k_cache: Tensor, v_cache: Tensor,
+        meta: AttentionMetadata,
+    ) -> Tensor:
+        """Decoder layer ``i`` (model/qwen3.py:112-122) for prefill-sized batches: int8 linears on the
+        LDS-tiled MFMA GEMM (silu * up in its epilogue; the o and down projections add the residual
+        and apply the next RMSNorm, merging split-K partials in the same pass) and q/k-norm + RoPE +
+        KV write as its own kernel. ``x`` is the residual stream (updated in place), ``h`` its
+        input RMSNorm; returns the next layer's normed input (the final norm after the last layer)."""
         cfg = self.cfg
         t = x.shape[0]
         layers = self.layers
-        h = kernels.rmsnorm(x, layers[0].input_layernorm.weight, layers[0].input_layernorm.eps)
-        for i, (layer, (k_cache, v_cache)) in enumerate(zip(layers, kv_caches, strict=True)):
-            attn, mlp = layer.self_attn, layer.mlp
-            qkv, o, gu, dn = attn.qkv_proj, attn.o_proj, mlp.gate_up_proj, mlp.down_proj
-            q = kernels.qk_norm_rope_cache(
-                kernels.int8_linear(h, qkv.qweight, qkv.scale), attn.num_heads, attn.num_kv_heads, attn.head_dim,
-                attn.q_norm.weight, attn.k_norm.weight, attn.q_norm.eps, cos, sin, meta.slot_mapping, k_cache, v_cache,
-            )
-            a = attend(q, k_cache, v_cache, meta, attn.scale).view(t, attn.q_size)
-            post = layer.post_attention_layernorm
-            hn = kernels.int8_linear_add_rmsnorm(a, o.qweight, o.scale, x, post.weight, post.eps)
-            act = kernels.int8_linear(hn, gu.qweight, gu.scale, kernels.EPI_SILU_MUL)
-            nxt = layers[i + 1].input_layernorm if i + 1 < len(layers) else self.norm
-            h = kernels.int8_linear_add_rmsnorm(act, dn.qweight, dn.scale, x, nxt.weight,
-                                                cfg.rms_norm_eps if nxt is self.norm else nxt.eps)
-        return h
+        layer = layers[i]
+        attn, mlp = layer.self_attn, layer.mlp
+        qkv, o, gu, dn = attn.qkv_proj, attn.o_proj, mlp.gate_up_proj, mlp.down_proj
+        q = kernels.qk_norm_rope_cache(
+            kernels.int8_linear(h, qkv.qweight, qkv.kscale), attn.num_heads, attn.num_kv_heads, attn.head_dim,
+            attn.q_norm.weight, attn.k_norm.weight, attn.q_norm.eps, cos, sin, meta.slot_mapping, k_cache, v_cache,
+        )
+        a = attend(q, k_cache, v_cache, meta, attn.scale).view(t, attn.q_size)
+        post = layer.post_attention_layernorm
+        hn = kernels.int8_linear_add_rmsnorm(a, o.qweight, o.kscale, x, post.weight, post.eps)
+        act = kernels.int8_linear(hn, gu.qweight, gu.kscale, kernels.EPI_SILU_MUL)
+        nxt = layers[i + 1].input_layernorm if i + 1 < len(layers) else self.norm
+        return kernels.int8_linear_add_rmsnorm(act, dn.qweight, dn.kscale, x, nxt.weight,
+                                               cfg.rms_norm_eps if nxt is self.norm else nxt.eps)
 
     def compute_logits(self, hidden: Tensor) -> Tensor:
         """[n, hidden] -> [n, vocab] float32, the product in bf16 (qwen3.py:155-158)."""

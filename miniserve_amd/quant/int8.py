@@ -1,7 +1,7 @@
 """Weight-only INT8 linears (reference: src/miniserve/quant/int8.py).
 
 Same storage as the reference -- ``qweight`` int8 ``[out, in]`` row-major and ``scale`` ``[out]``
-in the weight dtype (bf16), with scale = max|w_row| / 127 and q = round_half_even(w / scale) --
+in the weight dtype (bf16 for the models here), with scale = max|w_row| / 127 and q = round_half_even(w / scale) --
 but the pack runs as one HIP kernel on the GPU, bit-identical to quant/int8.py:27-32, and the
 forward never materializes the dequantized matrix: the HIP kernel dequantizes each weight in
 registers to the same bf16(q * s) value and multiplies on MFMA tiles.
@@ -16,7 +16,17 @@ from miniserve_amd import kernels
 
 
 class Int8Linear(nn.Module):
-    """Drop-in for quant/int8.py:21-37: ``Int8Linear(weight)``; ``forward(x) -> [..., out]``."""
+    """Drop-in for quant/int8.py:21-37: ``Int8Linear(weight)``; ``forward(x) -> [..., out]``.
+
+    Any floating weight on the GPU is accepted, as the reference accepts any (quant/int8.py:25-33):
+    it is packed from its float32 value (``weight.float()``; bf16 and float32 bits go to the kernel
+    as they are, float16 and float64 are converted first), so ``qweight`` is bit-identical to the
+    reference's and ``scale`` is held in the weight's dtype. The HIP forward multiplies bf16
+    activations with bf16 row scales: for a bf16 weight that is ``scale`` itself; for another
+    dtype ``scale`` is rounded to bf16 once here, and activations of another dtype are computed in
+    bf16 and returned in their own dtype (within the bf16 path's tolerance of the reference, not
+    bit-equal to its float32 dequantization). CPU weights are rejected: there is no CPU path.
+    """
 
     qweight: Tensor
     scale: Tensor
@@ -25,17 +35,41 @@ class Int8Linear(nn.Module):
         super().__init__()
         if not weight.is_cuda:
             raise RuntimeError("Int8Linear packs on the GPU: move the weight to the MI355X first")
-        if weight.dtype != torch.bfloat16:
-            raise RuntimeError(f"Int8Linear supports bf16 weights (got {weight.dtype})")
-        q, s = kernels.int8_quantize(weight)
+        if not weight.is_floating_point():
+            raise RuntimeError(f"Int8Linear needs a floating-point weight (got {weight.dtype})")
+        packed = weight if weight.dtype in (torch.bfloat16, torch.float32) else weight.detach().float()
+        q, s = kernels.int8_quantize(packed)
         self.register_buffer("qweight", q)
-        self.register_buffer("scale", s)
+        if weight.dtype == torch.bfloat16:
+            self.register_buffer("scale", s)
+            self._kscale = s
+        else:
+            # the float32 row scale (max|w| / 127, as the reference keeps it) in the weight dtype
+            w32 = packed.detach().float()
+            s32 = w32.abs().amax(dim=1).clamp(min=1e-8) / 127.0
+            self.register_buffer("scale", s32.to(weight.dtype))
+            self._kscale = s  # bf16(s32), for the kernels
         self.out_features, self.in_features = weight.shape
+
+    @property
+    def kscale(self) -> Tensor:
+        """The bf16 row scales the kernels multiply with (``scale`` itself for a bf16 weight)."""
+        return self._kscale
+
+    def _apply(self, fn, recurse=True):  # the kernels' scale follows the module's device, stays bf16
+        out = super()._apply(fn, recurse)
+        src = self.scale if self.scale.dtype == torch.bfloat16 else self._kscale
+        self._kscale = src.to(device=self.scale.device)
+        return out
 
     def forward(self, x: Tensor, epilogue: int = kernels.EPI_NONE, residual: Tensor | None = None) -> Tensor:
         """y = x @ bf16(qweight * scale)^T; ``epilogue`` fuses SwiGLU's silu(gate) * up or a
         residual add into the same kernel (used by this package's Qwen3 layers)."""
-        return kernels.int8_linear(x, self.qweight, self.scale, epilogue, residual)
+        if x.dtype == torch.bfloat16:
+            return kernels.int8_linear(x, self.qweight, self._kscale, epilogue, residual)
+        r = residual.to(torch.bfloat16) if residual is not None else None
+        y = kernels.int8_linear(x.to(torch.bfloat16), self.qweight, self._kscale, epilogue, r)
+        return y.to(x.dtype)
 
     def extra_repr(self) -> str:
         return f"in_features={self.in_features}, out_features={self.out_features}, int8 per-row"

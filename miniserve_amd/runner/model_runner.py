@@ -225,7 +225,10 @@ class ModelRunner:
         if self.use_graphs and self._graphable(scheduled):
             g = self.graphs.get(len(scheduled))
             if g is None:
-                g = self.graphs[len(scheduled)] = CapturedDecode(self, len(scheduled), self.max_model_len // self.block_size)
+                # positions up to max_model_len - 1 are graphable: ceil(max_model_len / block_size)
+                # table entries, the last block possibly partial
+                width = -(-self.max_model_len // self.block_size)
+                g = self.graphs[len(scheduled)] = CapturedDecode(self, len(scheduled), width)
             return [[t] for t in g.run(scheduled, self.block_size)]
         inp = self.prepare(scheduled)
         if inp.logits_rows.numel() == 0:

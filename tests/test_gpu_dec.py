@@ -2,13 +2,13 @@
 operand registers, RMSNorm prologue, embedding gather, residual / silu * up epilogues) against the
 CPU oracle on the same seeded inputs.
 
-The kernel multiplies the int8 weights exactly (as bf16 integers) and applies the row scale -- and
-the RMSNorm row factor -- to the finished dot products, where the reference rounds bf16(q * s) and
-bf16(w * bf16(x * r)) element by element first. Bars: within rel-L2 1e-2 of the oracle (the
-reference's rounding) and within bf16 output rounding (4e-3) of the float64 product of the same
-int8 values, scales and norm; gathered rows bit-exact; the residual add exact on the kernel's own
-projection; the fused norm within 8e-3 of the norm kernel followed by the plain product (the two
-round at different points); results bit-identical across calls. Every call goes through the C ABI.
+The kernel rounds where the reference rounds: weights dequantized to bf16(q * s), the RMSNorm
+prologue as bf16(w * bf16(x * r)), float32 accumulation, bf16 outputs. Bars: within rel-L2 2e-3 of
+the oracle (float32 summation order and the occasional rounding it flips); within bf16 output
+rounding (4e-3) of the float64 product of the same bf16 operands; gathered rows bit-exact; the
+residual add exact on the kernel's own projection; the fused norm within 2e-3 of the norm kernel
+followed by the plain product; results bit-identical across calls. Every call goes through the C
+ABI.
 """
 
 from __future__ import annotations
@@ -38,8 +38,8 @@ def _norm_w(dim, seed):
 
 
 def _exact_weights(q, s):
-    """float64 q * s: the int8 weights and scales without the reference's bf16 rounding."""
-    return q.double() * s.double()[:, None]
+    """The dequantized weights bf16(q * s) (quant/int8.py:36) in float64."""
+    return (q.to(torch.bfloat16) * s[:, None]).double()
 
 
 def _exact_norm(x, w, eps):
@@ -72,7 +72,7 @@ def test_dec_linear(m, n, k):
     assert torch.equal(y, y2)  # deterministic
     ref = oi.int8_linear(x, q, s)
     exact = x.double() @ _exact_weights(q, s).T
-    assert rel_l2(y.cpu(), ref) < 1e-2
+    assert rel_l2(y.cpu(), ref) < 2e-3
     assert rel_l2(y.cpu(), exact) < 4e-3
 
 
@@ -86,7 +86,7 @@ def test_dec_residual_in_place(m, n, k):
     out = kernels.int8_linear_dec(x.to(DEV), q.to(DEV), s.to(DEV), kernels.EPI_RESIDUAL, residual=rd, out=rd)
     assert out.data_ptr() == rd.data_ptr()
     ref = r + oi.int8_linear(x, q, s)
-    assert rel_l2(rd.cpu(), ref) < 1e-2
+    assert rel_l2(rd.cpu(), ref) < 2e-3
     y = kernels.int8_linear_dec(x.to(DEV), q.to(DEV), s.to(DEV)).cpu()
     assert torch.equal(rd.cpu(), r + y)  # the residual add itself is exact on the kernel's projection
 
@@ -105,14 +105,14 @@ def test_dec_silu_mul(m, k, with_norm):
     gate, up = oi.int8_linear(h, q, s).chunk(2, dim=-1)
     ref = torch.nn.functional.silu(gate) * up
     assert y.shape == (m, n // 2)
-    assert rel_l2(y.cpu(), ref) < 1e-2
+    assert rel_l2(y.cpu(), ref) < 2e-3
     h64 = _exact_norm(x, w, 1e-6) if with_norm else x.double()
     g64, u64 = (h64 @ _exact_weights(q, s).T).chunk(2, dim=-1)
     assert rel_l2(y.cpu(), torch.nn.functional.silu(g64) * u64) < 8e-3
     if with_norm:  # against the norm kernel followed by the plain fused product
         hd = kernels.rmsnorm(x.to(DEV), w.to(DEV), 1e-6)
         plain = kernels.int8_linear_dec(hd, q.to(DEV), s.to(DEV), kernels.EPI_SILU_MUL)
-        assert rel_l2(y.cpu(), plain.cpu()) < 8e-3
+        assert rel_l2(y.cpu(), plain.cpu()) < 2e-3
 
 
 @pytest.mark.parametrize("m,n,k", [(64, 4096, 1024), (1, 4096, 1024), (33, 6144, 4096)])
@@ -123,12 +123,12 @@ def test_dec_norm_prologue(m, n, k):
     w = _norm_w(k, seed=m + 8)
     y = kernels.int8_linear_dec(x.to(DEV), q.to(DEV), s.to(DEV), norm_w=w.to(DEV), eps=1e-6).cpu()
     h = ol.rms_norm(x, w, 1e-6)
-    assert rel_l2(y, oi.int8_linear(h, q, s)) < 1e-2
-    assert rel_l2(y, _exact_norm(x, w, 1e-6) @ _exact_weights(q, s).T) < 4e-3
-    # against the norm kernel (the reference's roundings) followed by the plain product
+    assert rel_l2(y, oi.int8_linear(h, q, s)) < 2e-3
+    assert rel_l2(y, _exact_norm(x, w, 1e-6) @ _exact_weights(q, s).T) < 6e-3
+    # against the norm kernel (the same roundings) followed by the plain product
     hd = kernels.rmsnorm(x.to(DEV), w.to(DEV), 1e-6)
     plain = kernels.int8_linear_dec(hd, q.to(DEV), s.to(DEV)).cpu()
-    assert rel_l2(y, plain) < 8e-3
+    assert rel_l2(y, plain) < 2e-3
 
 
 @pytest.mark.parametrize("t", [1, 64, 70])
@@ -146,7 +146,7 @@ def test_dec_gather_embedding(t):
     x = table[ids]
     assert torch.equal(resid.cpu(), x)  # the embedding rows, bit for bit
     h = ol.rms_norm(x, w, 1e-6)
-    assert rel_l2(y, oi.int8_linear(h, q, s)) < 1e-2
+    assert rel_l2(y, oi.int8_linear(h, q, s)) < 2e-3
     plain = kernels.int8_linear_dec(x.to(DEV), q.to(DEV), s.to(DEV), norm_w=w.to(DEV), eps=1e-6).cpu()
     assert torch.equal(y, plain)
 

@@ -269,6 +269,32 @@ def test_decode_attention_long_contexts_split():
     assert rel_l2(out, dense) < 1e-2
 
 
+def test_decode_attention_eight_waves_g1():
+    """G = 1 (8 query heads on 8 KV heads) with one split per sequence of 1024+ keys: 64 sequences
+    at contexts up to 2048 (64 x 8 workgroups, the eight-wavefront decode kernel)."""
+    rng = random.Random(11)
+    specs = [(rng.randint(128, 2048) - 1, 1) for _ in range(63)] + [(2047, 1)]
+    ptok, parts = kernels.decode_splits(64, 8, 2048 // 16)
+    assert parts == 1 and ptok >= 1024
+    out, ref, dense = _run_both(specs, 8, 8, seed=11)
+    for i in range(len(specs)):
+        assert rel_l2(out[i], ref[i]) < 1e-2, i
+    assert rel_l2(out, dense) < 1e-2
+
+
+def test_decode_attention_eight_waves_g1_split():
+    """G = 1 with contexts past 4096 keys in a batch of 32 x 8 workgroups: two workgroup-level
+    splits of 1024+ keys each (eight wavefronts) merged by the split-merge kernel."""
+    rng = random.Random(12)
+    specs = [(rng.randint(64, 4000), 1) for _ in range(28)] + [(4096, 1), (5000, 1), (7000, 1), (8191, 1)]
+    ptok, parts = kernels.decode_splits(32, 8, 8192 // 16)
+    assert parts >= 2 and ptok >= 1024
+    out, ref, dense = _run_both(specs, 8, 8, seed=12)
+    for i in range(len(specs)):
+        assert rel_l2(out[i], ref[i]) < 1e-2, i
+    assert rel_l2(out, dense) < 1e-2
+
+
 @pytest.mark.parametrize("heads,kv_heads", [(16, 8), (32, 8), (8, 8)])
 def test_prefill_attention(heads, kv_heads):
     # fresh prompts, a chunk after cached keys, speculative-verify-sized rows, ragged tiles

@@ -83,3 +83,27 @@ def test_rejection_sampling_keeps_the_target_distribution_on_gpu():
     assert chi_square(torch.bincount(first, minlength=v).double(), p[0].cpu().double()) < CHI2_DF4_P001
     second = nxt[acc == 1].cpu()
     assert chi_square(torch.bincount(second, minlength=v).double(), p[1].cpu().double()) < CHI2_DF4_P001
+
+
+def test_verify_sampled_converts_its_inputs():
+    """float64 probabilities, uniforms and noise and non-contiguous int64 drafts: every operand the
+    wrapper converts stays alive until the kernel has read it, so the result equals the call on
+    float32 contiguous copies (and the oracle's on the same values)."""
+    g = torch.Generator().manual_seed(7)
+    b, k, v = 33, 4, 30000
+    tp = torch.softmax(torch.randn(b, k + 1, v, generator=g, dtype=torch.float64) * 2, dim=-1)
+    q = torch.softmax(torch.randn(b, k, v, generator=g, dtype=torch.float64) * 2, dim=-1)
+    drafts_t = torch.randint(0, v, (k, b), generator=g)
+    drafts_t[:, ::2] = tp[::2, :k].argmax(-1).T
+    drafts = drafts_t.T  # [b, k], not contiguous
+    assert not drafts.is_contiguous()
+    nd = torch.randint(1, k + 1, (2 * b,), generator=g)[::2]  # strided too
+    u = torch.rand(b, k, generator=g, dtype=torch.float64)
+    noise = torch.empty(b, v, dtype=torch.float64).exponential_(generator=g)
+    acc, nxt = hrj.verify_sampled(tp.to(DEV), drafts.to(DEV), nd.to(DEV), q.to(DEV), u.to(DEV), noise.to(DEV))
+    tp32, q32, u32, n32 = tp.float(), q.float(), u.float(), noise.float()
+    acc2, nxt2 = hrj.verify_sampled(tp32.to(DEV), drafts.contiguous().to(DEV), nd.contiguous().to(DEV), q32.to(DEV),
+                                    u32.to(DEV), n32.to(DEV))
+    assert torch.equal(acc.cpu(), acc2.cpu()) and torch.equal(nxt.cpu(), nxt2.cpu())
+    racc, _ = orj.verify_sampled(tp32, drafts.contiguous(), nd.contiguous(), q32, u32, n32)
+    assert torch.equal(acc.cpu(), racc)
