@@ -226,6 +226,25 @@ int msa_paged_attention_decode(const uint16_t* q, int64_t ldq, const uint16_t* k
                                int partition_tokens, int max_partitions, float scale, uint16_t* out,
                                int64_t ldo, void* workspace, size_t workspace_bytes, msa_stream_t stream);
 
+/* Largest split-partials size (msa_paged_attention_decode_workspace_size) that
+ * msa_paged_attention_decode_noalloc serves: 16 MiB. */
+#define MSA_DECODE_NOALLOC_MAX_BYTES ((size_t)16 << 20)
+
+/* msa_paged_attention_decode without a workspace argument, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No
+ * counterpart in the reference. The split partials live in a scratch array inside the library, one
+ * per GPU, held until the process ends; calls whose partials need more than
+ * MSA_DECODE_NOALLOC_MAX_BYTES fail with MSA_ERR_WORKSPACE, and the call allocates nothing. Every
+ * call on one GPU shares that GPU's scratch: calls that overlap in time on one GPU (different
+ * streams) race and must be ordered by the caller. Results are bit-identical to
+ * msa_paged_attention_decode's for the same arguments. */
+int msa_paged_attention_decode_noalloc(const uint16_t* q, int64_t ldq, const uint16_t* k_cache,
+                                       const uint16_t* v_cache, int64_t num_slots, int heads, int kv_heads,
+                                       int head_dim, int block_size, const int32_t* block_tables, int max_blocks,
+                                       const int32_t* context_lens, const int32_t* q_rows, int num_seqs,
+                                       int partition_tokens, int max_partitions, float scale, uint16_t* out,
+                                       int64_t ldo, msa_stream_t stream);
+
 /* The decode rows of Qwen3Attention.forward from the projection onward (model/qwen3.py:95-99 with
  * the cache write of attention/backends.py:159-160) in one launch: qkv [*, (H + 2 KVH) * 128]
  * holds the int8 qkv projection rows [q | k | v] (row stride ldqkv, model/loader.py:22-28). For

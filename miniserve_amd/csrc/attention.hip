@@ -16,6 +16,8 @@
 // instructions) so each lane holds 8 scores of ONE query, applies the causal mask and an online
 // softmax with lane-local statistics, and accumulates O^T += V^T P^T (8 instructions) with P in
 // bf16.
+#include <mutex>
+
 #include "common.h"
 
 namespace msa {
@@ -752,6 +754,70 @@ static int decode_args(const char* who, const uint16_t* q, int64_t ldq, const ui
 }
 }  // namespace msa
 
+namespace msa {
+// The decode entry points' shared body: checks, launch of the decode kernel and, with splits, of
+// the split merge.
+static int decode_entry(const char* who, const uint16_t* q, int64_t ldq, const uint16_t* k_cache,
+                        const uint16_t* v_cache, int64_t num_slots, int heads, int kv_heads, int head_dim,
+                        int block_size, const int32_t* block_tables, int max_blocks, const int32_t* context_lens,
+                        const int32_t* q_rows, int num_seqs, int partition_tokens, int max_partitions, float scale,
+                        uint16_t* out, int64_t ldo, void* workspace, size_t workspace_bytes, hipStream_t s) {
+  DecodeArgs a;
+  int rc = decode_args(who, q, ldq, k_cache, v_cache, num_slots, heads, kv_heads, head_dim, block_size, block_tables,
+                       max_blocks, context_lens, q_rows, num_seqs, partition_tokens, max_partitions, scale, out, ldo,
+                       workspace, workspace_bytes, a);
+  if (rc != MSA_OK) return rc;
+  switch (heads / kv_heads) {
+    case 1: launch_decode<1>(a, num_seqs, s); break;
+    case 2: launch_decode<2>(a, num_seqs, s); break;
+    case 4: launch_decode<4>(a, num_seqs, s); break;
+    case 8: launch_decode<8>(a, num_seqs, s); break;
+    default: return fail(MSA_ERR_UNSUPPORTED, std::string(who) + ": heads / kv_heads must be 1, 2, 4 or 8");
+  }
+  rc = check_launch(who);
+  if (rc != MSA_OK || max_partitions == 1) return rc;
+  hipLaunchKernelGGL(paged_decode_reduce_kernel, dim3(num_seqs, heads), dim3(kHeadDim), 0, s, a);
+  return check_launch("paged attention decode (split merge)");
+}
+
+// Scratch of msa_paged_attention_decode_noalloc: the float32 split partials of one call. A
+// file-scope device array, one copy per GPU, which holds it until the process ends. In host code
+// its name is not a device address: each device's address comes from hipGetSymbolAddress, looked
+// up with that device current on the first call there, and only that address reaches kernels.
+constexpr size_t kDecodeScratchBytes = MSA_DECODE_NOALLOC_MAX_BYTES;
+static __device__ __align__(256) unsigned char scratch[kDecodeScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices] = {};
+
+// This device's scratch address (the stream's device; the current device for the null stream).
+static int decode_scratch(hipStream_t s, void** ptr) {
+  int dev = 0;
+  hipError_t e = s ? hipStreamGetDevice(s, &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(MSA_ERR_LAUNCH, std::string("decode scratch: device of the stream: ") + hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(MSA_ERR_UNSUPPORTED, "decode scratch: device index past 63");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    int cur = 0;
+    e = hipGetDevice(&cur);
+    if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
+    void* p = nullptr;
+    if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != dev) {
+      const hipError_t back = hipSetDevice(cur);
+      if (e == hipSuccess) e = back;
+    }
+    if (e != hipSuccess || p == nullptr)
+      return fail(MSA_ERR_LAUNCH, std::string("decode scratch: hipGetSymbolAddress: ") +
+                                      (e != hipSuccess ? hipGetErrorString(e) : "null address"));
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return MSA_OK;
+}
+}  // namespace msa
+
 extern "C" int msa_paged_attention_decode(const uint16_t* q, int64_t ldq, const uint16_t* k_cache, const uint16_t* v_cache,
                                           int64_t num_slots, int heads, int kv_heads, int head_dim, int block_size,
                                           const int32_t* block_tables, int max_blocks, const int32_t* context_lens,
@@ -760,23 +826,31 @@ extern "C" int msa_paged_attention_decode(const uint16_t* q, int64_t ldq, const 
                                           size_t workspace_bytes, msa_stream_t stream) {
   using namespace msa;
   if (num_seqs == 0) return MSA_OK;
-  DecodeArgs a;
-  int rc = decode_args("msa_paged_attention_decode", q, ldq, k_cache, v_cache, num_slots, heads, kv_heads, head_dim,
-                       block_size, block_tables, max_blocks, context_lens, q_rows, num_seqs, partition_tokens,
-                       max_partitions, scale, out, ldo, workspace, workspace_bytes, a);
-  if (rc != MSA_OK) return rc;
-  hipStream_t s = (hipStream_t)stream;
-  switch (heads / kv_heads) {
-    case 1: launch_decode<1>(a, num_seqs, s); break;
-    case 2: launch_decode<2>(a, num_seqs, s); break;
-    case 4: launch_decode<4>(a, num_seqs, s); break;
-    case 8: launch_decode<8>(a, num_seqs, s); break;
-    default: return fail(MSA_ERR_UNSUPPORTED, "msa_paged_attention_decode: heads / kv_heads must be 1, 2, 4 or 8");
+  return decode_entry("msa_paged_attention_decode", q, ldq, k_cache, v_cache, num_slots, heads, kv_heads, head_dim,
+                      block_size, block_tables, max_blocks, context_lens, q_rows, num_seqs, partition_tokens,
+                      max_partitions, scale, out, ldo, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+extern "C" int msa_paged_attention_decode_noalloc(const uint16_t* q, int64_t ldq, const uint16_t* k_cache,
+                                                  const uint16_t* v_cache, int64_t num_slots, int heads, int kv_heads,
+                                                  int head_dim, int block_size, const int32_t* block_tables,
+                                                  int max_blocks, const int32_t* context_lens, const int32_t* q_rows,
+                                                  int num_seqs, int partition_tokens, int max_partitions, float scale,
+                                                  uint16_t* out, int64_t ldo, msa_stream_t stream) {
+  using namespace msa;
+  if (num_seqs == 0) return MSA_OK;
+  const size_t need = msa_paged_attention_decode_workspace_size(num_seqs, heads, head_dim, max_partitions);
+  if (need > kDecodeScratchBytes)
+    return fail(MSA_ERR_WORKSPACE, "msa_paged_attention_decode_noalloc: the split partials need " + std::to_string(need) +
+                                       " bytes, more than the 16 MiB scratch (fewer sequences or partitions per call)");
+  void* ws = nullptr;
+  if (need > 0) {
+    const int rc = decode_scratch((hipStream_t)stream, &ws);
+    if (rc != MSA_OK) return rc;
   }
-  rc = check_launch("msa_paged_attention_decode");
-  if (rc != MSA_OK || max_partitions == 1) return rc;
-  hipLaunchKernelGGL(paged_decode_reduce_kernel, dim3(num_seqs, heads), dim3(kHeadDim), 0, s, a);
-  return check_launch("msa_paged_attention_decode (split merge)");
+  return decode_entry("msa_paged_attention_decode_noalloc", q, ldq, k_cache, v_cache, num_slots, heads, kv_heads,
+                      head_dim, block_size, block_tables, max_blocks, context_lens, q_rows, num_seqs, partition_tokens,
+                      max_partitions, scale, out, ldo, ws, need > 0 ? kDecodeScratchBytes : 0, (hipStream_t)stream);
 }
 
 extern "C" int msa_paged_attention_decode_qkv(const uint16_t* qkv, int64_t ldqkv, const uint16_t* q_norm_w,

@@ -72,6 +72,11 @@ def test_argument_errors_are_reported():
         "msa_paged_attention_prefill", FAKE, 128 * 8, FAKE, FAKE, 16, 8, 1, 128, 16, FAKE, 1, FAKE, FAKE, 1, 1.0,
         FAKE, 128 * 8, NULL,
     )
+    # the allocation-free decode entry point refuses partials larger than its 16 MiB scratch
+    assert "16 MiB scratch" in _err(
+        "msa_paged_attention_decode_noalloc", FAKE, 128 * 32, FAKE, FAKE, 16, 32, 8, 128, 16, FAKE, 256, FAKE, FAKE,
+        2048, 64, 64, 1.0, FAKE, 128 * 32, NULL,
+    )
     assert "head_dim must be even" in _err(
         "msa_qk_norm_rope_cache", FAKE, 64, 1, 2, 1, 7, FAKE, FAKE, 1e-6, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, NULL
     )
