@@ -46,9 +46,8 @@ BATCH, CTX_LO, CTX_HI = 64, 256, 384
 # from rocprofv3 --pmc: 42,902.07 KiB x 2 x 1024 + 512 KiB x 1024
 # (profiles/paged_decode_kernel_traffic_pmc.md).
 ATTN_TRAFFIC_BYTES: int | None = 88_321_135
-# The same counters over one layer's four decode linears (profiles/dec_linear_kernel_pmc.md); None
-# until measured.
-LINEAR_TRAFFIC_BYTES: int | None = None
+# The same counters over one layer's four decode linears, summed (profiles/dec_linear_kernel_pmc.md).
+LINEAR_TRAFFIC_BYTES: int | None = 25_925_165
 
 
 def log(msg: str) -> None:
@@ -661,8 +660,11 @@ def bench_decode8b(args) -> dict:
 def kernel_only(mode: str, seed: int) -> int:
     """``attention``: only the decode-attention timing of the decode workload; ``linear``: the int8
     linears of the decode step (plus the single gate_proj-shaped linear) over rotated weights;
-    ``copy``: a 256 MiB copy, 10 times (a kernel of known traffic, to calibrate rocprofv3's
-    FETCH_SIZE / WRITE_SIZE)."""
+    ``step-linears``: the four decode linears of every layer of the 0.6B model as the decode step
+    runs them; ``gemm``: the chunked-prefill step's gate_up GEMM at 2048 tokens over every layer's
+    weights; ``prefill-attention``: its paged attention (a 1984-token chunk after 64 decodes) over
+    28 KV pools; ``copy``: a 256 MiB copy, 10 times (a kernel of known traffic, to calibrate
+    rocprofv3's FETCH_SIZE / WRITE_SIZE)."""
     import torch
 
     from miniserve_amd import kernels, workloads
@@ -676,6 +678,43 @@ def kernel_only(mode: str, seed: int) -> int:
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_each_way": src.numel() * 2, "copies": 10}))
+        return 0
+    if mode == "step-linears":  # the four decode linears of every layer, as the decode step runs them
+        model, _ = build_int8_model(workloads.QWEN3_0_6B, seed, dev, 4096, on_device=True)
+        for name, t, b in time_layer_linears(model, BATCH, dev):
+            print(json.dumps({"linear": name, "us_per_launch": round(t * 1e6, 3), "bytes_per_launch": b,
+                              "GB_s": round(b / t / 1e9, 1)}), flush=True)
+        return 0
+    if mode in ("gemm", "prefill-attention"):  # the chunked-prefill step's dominant kernels
+        cfg = workloads.QWEN3_0_6B
+        if mode == "gemm":
+            model, _ = build_int8_model(cfg, seed, dev, 4096, on_device=True)
+            h = torch.randn(2048, cfg["hidden_size"], device=dev).to(torch.bfloat16)
+            y = torch.empty(2048, cfg["intermediate_size"], dtype=torch.bfloat16, device=dev)
+            lin = [layer.mlp.gate_up_proj for layer in model.layers]
+            secs = hip_time(lambda i: kernels.int8_linear(h, lin[i].qweight, lin[i].kscale, kernels.EPI_SILU_MUL,
+                                                          out=y), len(lin))
+            flops = 2 * 2048 * 2 * cfg["intermediate_size"] * cfg["hidden_size"]
+            print(json.dumps({"kernel": "gate_up GEMM, M=2048", "us_per_launch": secs * 1e6,
+                              "TFLOP_s": flops / secs / 1e12}))
+            return 0
+        from miniserve_amd.attention import backends as hb
+
+        dec = workloads.decode_batch(64, 64, 1024, seed=seed + 1, spare_blocks=0)
+        chunk = 1984
+        blocks = dec.num_blocks + -(-chunk // 16)
+        layers = 28
+        kv = torch.empty(layers, 2, blocks * 16, 8, 128, dtype=torch.bfloat16, device=dev)
+        workloads.fill_kv_pool_(kv, seed=seed + 2, on_device=True)
+        chunks = [hb.SeqChunk(i, 1, c - 1, t) for i, (c, t) in enumerate(zip(dec.context_lens, dec.block_tables))]
+        chunks.append(hb.SeqChunk(64, chunk, 0, list(range(dec.num_blocks, blocks))))
+        slots = torch.tensor(dec.slot_mapping + [dec.num_blocks * 16 + p for p in range(chunk)], device=dev)
+        meta = hb.build_attention_metadata(chunks, slots, 16)
+        q = torch.randn(64 + chunk, 16, 128, device=dev).to(torch.bfloat16)
+        secs = hip_time(lambda i: hb.attend(q, kv[i, 0], kv[i, 1], meta, 128**-0.5), layers)
+        flops = 4 * 16 * 128 * (chunk * (chunk + 1) // 2) + 4 * 16 * 128 * sum(dec.context_lens)
+        print(json.dumps({"kernel": "paged attention, 1984-token chunk + 64 decodes", "us_per_launch": secs * 1e6,
+                          "TFLOP_s": flops / secs / 1e12}))
         return 0
     if mode == "linear":
         g = torch.Generator(device=dev).manual_seed(seed)
@@ -806,7 +845,8 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="decode")
-    ap.add_argument("--kernel-only", choices=["attention", "linear", "copy"], help="profiling entry point")
+    ap.add_argument("--kernel-only", choices=["attention", "linear", "copy", "step-linears", "gemm", "prefill-attention"],
+                    help="profiling entry point")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
