@@ -220,14 +220,36 @@ __global__ __launch_bounds__(64 * W) void paged_decode_kernel(DecodeArgs a) {
       sn[8 * hf + 4] = s1.x; sn[8 * hf + 5] = s1.y; sn[8 * hf + 6] = s1.z; sn[8 * hf + 7] = s1.w;
     }
     constexpr int kRounds = (G + 1 + 7) / 8;
+    // Round 0's vector and norm weights are loaded before the first K / V block, which then
+    // streams in while the norms and RoPE are computed (the loads complete in issue order, so
+    // waiting for these does not wait for the block).
+    uint32_t mine0[8];
+    uint4 nw0lo, nw0hi;
+    {
+      const int vi = min(rp, G);
+      const bool is_k = vi == G;
+      load8(qrow_p + (int64_t)(is_k ? a.heads + kvh : kvh * G + vi) * kHeadDim + 8 * dg, mine0);
+      const uint16_t* nw = is_k ? a.kn_w : a.qn_w;
+      nw0lo = *(const uint4*)(nw + 8 * dg);
+      nw0hi = *(const uint4*)(nw + 64 + 8 * dg);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    load_block(ph0, bfirst < a.max_blocks, ka, va);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int round = 0; round < kRounds; ++round) {
       const int vi = min(round * 8 + rp, G);  // groups past the last vector redo the key (unused)
       const bool is_k = vi == G;
       uint32_t mine[8];
-      load8(qrow_p + (int64_t)(is_k ? a.heads + kvh : kvh * G + vi) * kHeadDim + 8 * dg, mine);
-      const uint16_t* nw = is_k ? a.kn_w : a.qn_w;
-      norm_rope16(mine, *(const uint4*)(nw + 8 * dg), *(const uint4*)(nw + 64 + 8 * dg), c, sn, a.qk_eps);
+      if (round == 0) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) mine[e] = mine0[e];
+        norm_rope16(mine, nw0lo, nw0hi, c, sn, a.qk_eps);
+      } else {
+        load8(qrow_p + (int64_t)(is_k ? a.heads + kvh : kvh * G + vi) * kHeadDim + 8 * dg, mine);
+        const uint16_t* nw = is_k ? a.kn_w : a.qn_w;
+        norm_rope16(mine, *(const uint4*)(nw + 8 * dg), *(const uint4*)(nw + 64 + 8 * dg), c, sn, a.qk_eps);
+      }
 #pragma unroll
       for (int v = round * 8; v < min(round * 8 + 8, G + 1); ++v) {
         const int src = (v - round * 8) * 8 + dg;  // lane holding vector v's dims for this dg
@@ -247,7 +269,7 @@ __global__ __launch_bounds__(64 * W) void paged_decode_kernel(DecodeArgs a) {
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[h][e] = 0.f;
   }
-  load_block(ph0, bfirst < a.max_blocks, ka, va);  // before the context length is checked
+  if constexpr (!QKV) load_block(ph0, bfirst < a.max_blocks, ka, va);  // before the context length is checked
   if (start >= ctx) return;  // the reduce kernel merges only splits that hold keys
   // Fused: the cache is read for the keys before the new token, which comes from registers.
   const int end = min(QKV ? ctx - 1 : ctx, start + a.part_tokens);

@@ -310,19 +310,26 @@ def reshape_and_cache(k: Tensor, v: Tensor, k_cache: Tensor, v_cache: Tensor, sl
 # ---- paged attention ------------------------------------------------------------------------------
 
 
-DECODE_MAX_PART_BLOCKS = 256  # 16-token blocks per decode split (64 per wavefront)
+DECODE_MAX_PART_TOKENS = 4096  # keys per decode split: 64 blocks per wavefront of a four-wavefront workgroup
 
 
 def decode_splits(num_seqs: int, kv_heads: int, max_blocks: int) -> tuple[int, int]:
-    """(partition_tokens, partitions) for the decode kernel: one workgroup of four wavefronts per
-    (sequence, KV head) when that gives 256+ workgroups; otherwise split each sequence's keys
-    across workgroups (at least four 16-token blocks, one per wavefront, in each). A split holds
-    at most 256 blocks (4096 keys)."""
+    """(partition_tokens, partitions) for the decode kernel.
+
+    The keys per split depend only on the batch's (sequence, KV head) count, never on its
+    contexts or on the block-table width, so a step captured in a graph (tables padded to the
+    longest context the graph accepts) and the same step run eagerly split every sequence at
+    the same keys and sum in the same order: one split per sequence (up to 4096 keys) when the
+    pairs alone give 256+ workgroups; otherwise splits sized for about 512 workgroups at 1024-key
+    contexts, at least four 16-token blocks (one per wavefront). ``partitions`` only sizes the
+    grid to cover the table width; a sequence uses ceil(context / partition_tokens) of them."""
     wgs = max(1, num_seqs * kv_heads)
-    splits = 1 if wgs >= 256 else min(-(-512 // wgs), max(1, max_blocks // 4))
-    splits = max(splits, -(-max_blocks // DECODE_MAX_PART_BLOCKS))
-    per_blocks = -(-max_blocks // splits)
-    return per_blocks * 16, -(-max_blocks // per_blocks)
+    if wgs >= 256:
+        part = DECODE_MAX_PART_TOKENS
+    else:
+        blocks = max(4, -(-1024 * wgs // (512 * 16)))
+        part = 16 * min(1 << (blocks - 1).bit_length(), DECODE_MAX_PART_TOKENS // 16)
+    return part, max(1, -(-max_blocks * 16 // part))
 
 
 def paged_attention_decode(

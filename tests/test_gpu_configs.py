@@ -7,7 +7,7 @@
   oracle's layer (model/qwen3.py:112-122) on the same input.
 * Qwen3-8B shapes: one decoder layer at 256 decode tokens with contexts U[512, 4096] on the GEMM
   layer pipeline the 8B step runs (G = 4, the block table padded to the width a graph captured
-  for 4096 + 16 positions holds, so keys are split across two workgroups), its attention against
+  for 4096 + 16 positions holds), its attention with keys split across workgroups against
   float64, the gate_up linear [24576 x 4096] at 256 tokens, and the untied LM head's argmax at
   256 x 151936 x 4096.
 
@@ -194,12 +194,12 @@ def layer8b():
 def test_qwen3_8b_layer_256_decodes(layer8b):
     """The 8B-shaped layer as the 8B decode step runs it: 256 tokens with an intermediate size of
     12288 take the GEMM layer pipeline (int8 GEMMs, split-K merges with the residual and the next
-    RMSNorm, q/k-norm + RoPE + KV write, G = 4 decode attention with the keys of every context over
-    2064 split across two workgroups and merged) -- against the oracle's layer on the same input;
-    the K / V rows written match the oracle's."""
+    RMSNorm, q/k-norm + RoPE + KV write, G = 4 decode attention over the graph-padded table: two
+    partitions, the second empty, merged by the split-merge kernel) -- against the oracle's layer on
+    the same input; the K / V rows written match the oracle's."""
     runner, ocfg, ow, okv, rot, sched, inp, batch = layer8b
-    assert kernels.decode_splits(NSEQ_8B, 8, WIDTH_8B)[1] == 2
-    assert max(batch.context_lens) > 2064 * 1.5 and sum(c > 2064 for c in batch.context_lens) > 64
+    assert kernels.decode_splits(NSEQ_8B, 8, WIDTH_8B) == (4096, 2)  # the padded width's second split
+    assert max(batch.context_lens) > 3000 and sum(c > 2064 for c in batch.context_lens) > 64
     model = runner.model
     assert not model._token_split_ok(NSEQ_8B)
     step = om.prepare([(s.token_ids, s.num_computed, s.num_new, s.block_table) for s in sched], 16)
@@ -226,8 +226,9 @@ def test_qwen3_8b_layer_256_decodes(layer8b):
 
 def test_qwen3_8b_decode_attention_split_g4(layer8b):
     """G = 4 decode attention (32 q / 8 KV heads) at 256 sequences x U[512, 4096] through the
-    padded table (two workgroup-level splits of 2064 keys): against the oracle on every row and
-    float64 on the rows whose contexts sit at the split boundary, past it and near 4096."""
+    padded table, keys split across workgroups every 2048 keys and merged: against the oracle on
+    every row and float64 on the rows whose contexts sit at the split boundary, past it and near
+    4096."""
     runner, ocfg, ow, okv, rot, sched, inp, batch = layer8b
     d = inp.attn.decode
     heads, kvh, dim = 32, 8, 128
@@ -235,8 +236,9 @@ def test_qwen3_8b_decode_attention_split_g4(layer8b):
     q = torch.randn(NSEQ_8B, heads, dim, generator=g).to(torch.bfloat16)
     kc, vc = okv[0]  # the oracle's pool copy (the layer test may have written this step's keys)
     kcg, vcg = kc.to(DEV), vc.to(DEV)
-    ptok, parts = kernels.decode_splits(NSEQ_8B, kvh, WIDTH_8B)
-    assert parts == 2
+    # keys split across two workgroups at 2048 (the kernel takes any multiple of 16 up to 4096)
+    ptok, parts = 2048, -(-WIDTH_8B * 16 // 2048)
+    assert parts == 3
     out = torch.empty_like(q, device=DEV)
     kernels.paged_attention_decode(q.to(DEV), kcg, vcg, d.block_tables, d.context_lens, d.q_rows, ptok, parts,
                                    dim**-0.5, out)
@@ -249,7 +251,7 @@ def test_qwen3_8b_decode_attention_split_g4(layer8b):
     assert rel_l2(out, ref) < 1e-2
     ctx = batch.context_lens
     picks = sorted(set(
-        [min(range(NSEQ_8B), key=lambda i: abs(ctx[i] - t)) for t in (2064, 2065, 2080, 4096, 3000)] + list(range(4))))
+        [min(range(NSEQ_8B), key=lambda i: abs(ctx[i] - t)) for t in (2048, 2049, 2064, 4096, 3000)] + list(range(4))))
     for i in picks:
         assert rel_l2(out[i], ref[i]) < 1e-2, (i, ctx[i])
     idx, dense = _selected_rows_dense(q, kc, vc, [chunks[i] for i in picks], [[0]] * len(picks), dim**-0.5)

@@ -275,10 +275,13 @@ def test_qwen3_0_6b_greedy_ids_over_steps(seed):
     print(f"greedy identity over 3 steps, seed {seed}: {totals}")
 
 
-@pytest.mark.parametrize("batch", [5, 64])
+@pytest.mark.parametrize("batch", [5, 64, 192])
 def test_captured_decode_matches_eager(batch):
     """The HIP-graph decode step returns the eager step's ids on every replay, with eager work
-    and synchronizations between replays and new metadata (one more token) each step."""
+    and synchronizations between replays and new metadata (one more token) each step. The graph's
+    block tables are padded to max_model_len while the eager step's fit the contexts: the decode
+    splits depend on neither, so both sum in the same order (192 sequences: more than the decode
+    linear's 128 tokens, the plain attention path with eight-wavefront workgroups)."""
     weights = workloads.random_weights(SMALL, seed=7, norm_jitter=0.1)
     model = workloads.build_model(SMALL, weights, DEV, 512)
     quantize_int8_(model)
@@ -300,6 +303,8 @@ def test_captured_decode_matches_eager(batch):
         torch.cuda.synchronize()
         graph = runner.execute(seqs)
         assert [g[0] for g in graph] == eager, step
+        if batch > kernels.DEC_MAX_TOKENS:
+            assert kernels.decode_splits(batch, SMALL["num_key_value_heads"], 512 // 16)[0] >= 1024
         assert len(runner.graphs) == 1
         seqs = [ScheduledChunk(s.token_ids + [eager[i]], len(s.token_ids), 1, s.block_table) for i, s in enumerate(seqs)]
 
