@@ -205,7 +205,7 @@ def time_layer_attention(runner, sched, cfg, fused: bool = True) -> tuple[float,
     d = inp.attn.decode
     dev = runner.device
     heads, kvh, dim = cfg["num_attention_heads"], cfg["num_key_value_heads"], cfg["head_dim"]
-    ptok, parts = kernels.decode_splits(d.num_seqs, kvh, d.block_tables.shape[1])
+    ptok, parts = kernels.decode_splits(d.num_seqs, kvh, d.block_tables.shape[1], heads // kvh)
     g = torch.Generator(device=dev).manual_seed(5)
     out = torch.empty(len(sched), heads, dim, dtype=torch.bfloat16, device=dev)
     caches = runner.kv_caches
@@ -481,7 +481,7 @@ def bench_attention(args) -> dict:
     ctx = b.context_lens
     op_bytes = 4096 * sum(ctx) + 786_432 + 4 * sum(-(-c // 16) for c in ctx) + 256
     d = meta.decode
-    ptok, parts = kernels.decode_splits(nseq, kvh, d.block_tables.shape[1])
+    ptok, parts = kernels.decode_splits(nseq, kvh, d.block_tables.shape[1], heads // kvh)
     out_t = torch.empty_like(q)
 
     def kern(i):

@@ -151,7 +151,7 @@ def attend(q: Tensor, k_cache: Tensor, v_cache: Tensor, meta: AttentionMetadata,
     heads, kv_heads = q.shape[1], k_cache.shape[1]
     if meta.decode is not None:
         d = meta.decode
-        ptok, parts = kernels.decode_splits(d.num_seqs, kv_heads, d.block_tables.shape[1])
+        ptok, parts = kernels.decode_splits(d.num_seqs, kv_heads, d.block_tables.shape[1], heads // kv_heads)
         kernels.paged_attention_decode(
             q, k_cache, v_cache, d.block_tables, d.context_lens, d.q_rows, ptok, parts, scale, out, meta.block_size
         )
@@ -187,7 +187,7 @@ def attend_decode_qkv(
     d = meta.decode
     kv_heads, dim = k_cache.shape[1], k_cache.shape[2]
     out = torch.empty(qkv.shape[0], heads, dim, dtype=qkv.dtype, device=qkv.device)
-    ptok, parts = kernels.decode_splits(d.num_seqs, kv_heads, d.block_tables.shape[1])
+    ptok, parts = kernels.decode_splits(d.num_seqs, kv_heads, d.block_tables.shape[1], heads // kv_heads)
     kernels.paged_attention_decode_qkv(
         qkv, heads, q_norm_w, k_norm_w, qk_eps, cos_table, sin_table, meta.slot_mapping, k_cache, v_cache, d.block_tables,
         d.context_lens, d.q_rows, ptok, parts, scale, out, meta.block_size,

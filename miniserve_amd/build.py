@@ -46,10 +46,12 @@ def hipcc() -> str:
     return path
 
 
-# Per-file extra flags. attention.hip: keep MFMA accumulators in ordinary VGPRs -- the prefill
+# Per-file extra flags: keep MFMA accumulators in ordinary VGPRs. attention.hip: the prefill
 # kernel rescales its output accumulators between MFMAs every key tile, and in accumulation
-# registers each rescale costs a copy out and a copy back.
-EXTRA_FLAGS = {"attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+# registers each rescale costs a copy out and a copy back. gemm_int8.hip: in accumulation
+# registers the GEMM's main loop spends 48 VALU copies per two K steps shuffling accumulators.
+_VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
+EXTRA_FLAGS = {"attention.hip": _VGPR_FORM, "gemm_int8.hip": _VGPR_FORM}
 
 
 def _compile(src: str) -> Path:

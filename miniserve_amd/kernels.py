@@ -313,19 +313,21 @@ def reshape_and_cache(k: Tensor, v: Tensor, k_cache: Tensor, v_cache: Tensor, sl
 DECODE_MAX_PART_TOKENS = 4096  # keys per decode split: 64 blocks per wavefront of a four-wavefront workgroup
 
 
-def decode_splits(num_seqs: int, kv_heads: int, max_blocks: int) -> tuple[int, int]:
-    """(partition_tokens, partitions) for the decode kernel.
+def decode_splits(num_seqs: int, kv_heads: int, max_blocks: int, group: int) -> tuple[int, int]:
+    """(partition_tokens, partitions) for the decode kernel (``group`` = query heads per KV head).
 
-    The keys per split depend only on the batch's (sequence, KV head) count, never on its
-    contexts or on the block-table width, so a step captured in a graph (tables padded to the
-    longest context the graph accepts) and the same step run eagerly split every sequence at
-    the same keys and sum in the same order: one split per sequence (up to 4096 keys) when the
-    pairs alone give 256+ workgroups; otherwise splits sized for about 512 workgroups at 1024-key
-    contexts, at least four 16-token blocks (one per wavefront). ``partitions`` only sizes the
-    grid to cover the table width; a sequence uses ceil(context / partition_tokens) of them."""
+    The keys per split depend only on the batch's shape -- its (sequence, KV head) count and the
+    group size -- never on its contexts or on the block-table width, so a step captured in a graph
+    (tables padded to the longest context the graph accepts) and the same step run eagerly split
+    every sequence at the same keys and sum in the same order. When the pairs alone give 256+
+    workgroups: one split per sequence up to 4096 keys for groups of up to two query heads; for
+    larger groups (four-wavefront workgroups only) 2048-key splits, so that no wavefront walks more
+    than 32 blocks. Otherwise splits sized for about 512 workgroups at 1024-key contexts, at least
+    four 16-token blocks (one per wavefront). ``partitions`` only sizes the grid to cover the table
+    width; a sequence uses ceil(context / partition_tokens) of them."""
     wgs = max(1, num_seqs * kv_heads)
     if wgs >= 256:
-        part = DECODE_MAX_PART_TOKENS
+        part = DECODE_MAX_PART_TOKENS if group <= 2 else DECODE_MAX_PART_TOKENS // 2
     else:
         blocks = max(4, -(-1024 * wgs // (512 * 16)))
         part = 16 * min(1 << (blocks - 1).bit_length(), DECODE_MAX_PART_TOKENS // 16)

@@ -262,7 +262,7 @@ def test_decode_attention_long_contexts_split():
     contexts alone would take no split: the host splits every sequence's keys in 4096-key pieces."""
     rng = random.Random(5)
     specs = [(rng.randint(0, 300), 1) for _ in range(27)] + [(4094, 1), (4095, 1), (4096, 1), (6000, 1), (8191, 1)]
-    assert kernels.decode_splits(32, 8, 8192 // 16)[1] >= 2
+    assert kernels.decode_splits(32, 8, 8192 // 16, 2)[1] >= 2
     out, ref, dense = _run_both(specs, 16, 8, seed=5)
     for i in range(len(specs)):
         assert rel_l2(out[i], ref[i]) < 1e-2, i
@@ -274,7 +274,7 @@ def test_decode_attention_eight_waves_g1():
     at contexts up to 2048 (64 x 8 workgroups, the eight-wavefront decode kernel)."""
     rng = random.Random(11)
     specs = [(rng.randint(128, 2048) - 1, 1) for _ in range(63)] + [(2047, 1)]
-    ptok, parts = kernels.decode_splits(64, 8, 2048 // 16)
+    ptok, parts = kernels.decode_splits(64, 8, 2048 // 16, 1)
     assert parts == 1 and ptok >= 1024
     out, ref, dense = _run_both(specs, 8, 8, seed=11)
     for i in range(len(specs)):
@@ -287,7 +287,7 @@ def test_decode_attention_eight_waves_g1_split():
     splits of 1024+ keys each (eight wavefronts) merged by the split-merge kernel."""
     rng = random.Random(12)
     specs = [(rng.randint(64, 4000), 1) for _ in range(28)] + [(4096, 1), (5000, 1), (7000, 1), (8191, 1)]
-    ptok, parts = kernels.decode_splits(32, 8, 8192 // 16)
+    ptok, parts = kernels.decode_splits(32, 8, 8192 // 16, 1)
     assert parts >= 2 and ptok >= 1024
     out, ref, dense = _run_both(specs, 8, 8, seed=12)
     for i in range(len(specs)):
@@ -397,7 +397,7 @@ def test_decode_attention_split_across_workgroups(heads, kv_heads, ptok):
         kernels.paged_attention_decode(q.to(DEV), kcg, vcg, d.block_tables, d.context_lens, d.q_rows, ptok, parts,
                                        scale, out)
         assert rel_l2(out.cpu(), ref) < 1e-2
-    assert kernels.decode_splits(2, 8, 256)[1] > 1  # the host picks splits for small batches
+    assert kernels.decode_splits(2, 8, 256, 2)[1] > 1  # the host picks splits for small batches
 
 
 @pytest.mark.parametrize("heads,kv_heads,ptok", [(16, 8, 0), (32, 8, 0), (8, 8, 0), (16, 8, 32), (16, 4, 64)])

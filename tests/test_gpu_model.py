@@ -304,7 +304,7 @@ def test_captured_decode_matches_eager(batch):
         graph = runner.execute(seqs)
         assert [g[0] for g in graph] == eager, step
         if batch > kernels.DEC_MAX_TOKENS:
-            assert kernels.decode_splits(batch, SMALL["num_key_value_heads"], 512 // 16)[0] >= 1024
+            assert kernels.decode_splits(batch, SMALL["num_key_value_heads"], 512 // 16, 2)[0] >= 1024
         assert len(runner.graphs) == 1
         seqs = [ScheduledChunk(s.token_ids + [eager[i]], len(s.token_ids), 1, s.block_table) for i, s in enumerate(seqs)]
 

@@ -44,7 +44,7 @@ def _case(num_seqs, max_ctx, heads, kv_heads, seed):
 
 def _both(num_seqs, max_ctx, heads, kv_heads, seed):
     q, kc, vc, tables, ctx, rows = _case(num_seqs, max_ctx, heads, kv_heads, seed)
-    ptok, parts = kernels.decode_splits(num_seqs, kv_heads, tables.shape[1])
+    ptok, parts = kernels.decode_splits(num_seqs, kv_heads, tables.shape[1], heads // kv_heads)
     assert parts > 1  # the split partials go through the scratch
     stream = ctypes.c_void_p(torch.cuda.current_stream(DEV).cuda_stream)
     args = (_ptr(q), q.stride(0), _ptr(kc), _ptr(vc), kc.shape[0], heads, kv_heads, 128, 16, _ptr(tables),
