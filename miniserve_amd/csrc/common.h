@@ -50,6 +50,13 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
+// RMSNorm of a bf16 pair as model/layers.py:18-22 rounds it: bf16(w * bf16(x * r)). wlo / whi are
+// the norm weight pair with the other half zeroed, so v_dot2_f32_bf16 gives each product exactly.
+__device__ __forceinline__ uint32_t norm_pair(uint32_t xv, uint32_t wlo, uint32_t whi, float r) {
+  const uint32_t xr = pack_bf16x2(bf16lo(xv) * r, bf16hi(xv) * r);
+  return pack_bf16x2(dot2_bf16(xr, wlo, 0.f), dot2_bf16(xr, whi, 0.f));
+}
+
 // Eight int8 weights (bytes of lo, then hi, little-endian) dequantized to bf16(q * s) -- the value
 // of the reference's whole-matrix dequantization (quant/int8.py:36): a sign-extending byte
 // conversion, one multiply and half a packed conversion per weight.

@@ -65,13 +65,6 @@ struct DecLinArgs {
 };
 
 
-// RMSNorm of a bf16 pair as model/layers.py:18-22 rounds it: bf16(w * bf16(x * r)). wlo / whi are
-// the norm weight pair with the other half zeroed, so v_dot2_f32_bf16 gives each product exactly.
-__device__ __forceinline__ uint32_t norm_pair(uint32_t xv, uint32_t wlo, uint32_t whi, float r) {
-  const uint32_t xr = pack_bf16x2(bf16lo(xv) * r, bf16hi(xv) * r);
-  return pack_bf16x2(dot2_bf16(xr, wlo, 0.f), dot2_bf16(xr, whi, 0.f));
-}
-
 // Weight row of tile nt, lane row j. SILU_MUL: tiles [0, NT/2) are gate rows, [NT/2, NT) the
 // matching up rows (second half of the fused [gate | up] weight, model/loader.py:41-48).
 template <int NT, int EPI>
@@ -399,10 +392,19 @@ static int dec_dispatch(const DecShape& sh, const DecLinArgs& a, hipStream_t s) 
 
 bool dec_linear_supported(int64_t k) { return dec_kw(k) != 0; }
 
+// The streaming kernel (gemv_stream.hip) for up to 16 tokens over weight matrices with enough
+// 16-row tiles to give every CU a run of them.
+bool dec_stream_eligible(int64_t m, int64_t k, int64_t n, int epilogue);
+int launch_dec_stream(const uint16_t* x, int64_t ldx, int64_t m, int64_t k, const uint16_t* norm_w, float eps,
+                      const int8_t* qweight, const uint16_t* scale, int64_t n, int epilogue, uint16_t* y, int64_t ldy,
+                      const uint16_t* residual, int64_t ldr, hipStream_t s);
+
 int launch_dec_linear(const uint16_t* x, int64_t ldx, int64_t x_rows, const int64_t* gather, uint16_t* x_copy,
                       int64_t ld_copy, int64_t m, int64_t k, const uint16_t* norm_w, float eps, const int8_t* qweight,
                       const uint16_t* scale, int64_t n, int epilogue, uint16_t* y, int64_t ldy,
                       const uint16_t* residual, int64_t ldr, hipStream_t s) {
+  if (gather == nullptr && !(norm_w != nullptr && epilogue == DL_EPI_RESIDUAL) && dec_stream_eligible(m, k, n, epilogue))
+    return launch_dec_stream(x, ldx, m, k, norm_w, eps, qweight, scale, n, epilogue, y, ldy, residual, ldr, s);
   const DecShape sh = dec_shape(m, k, epilogue);
   if (sh.kw == 0) return fail(MSA_ERR_UNSUPPORTED, "decode linear: in_features must be 1024, 2048, 3072 or 4096");
   const int np = epilogue == DL_EPI_SILU_MUL ? sh.nt / 2 : sh.nt;
