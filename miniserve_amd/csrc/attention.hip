@@ -101,15 +101,11 @@ __device__ __forceinline__ float group8_sum(float v) {
 // Across the 8 row-pair groups of a wavefront (values are uniform within each 8-lane group).
 __device__ __forceinline__ float rowpair_max(float v) {
   v = fmaxf(v, dpp<0x140>(v));  // row_mirror: group g <-> the other group of its 16-lane row
-  v = fmaxf(v, __shfl_xor(v, 16));
-  v = fmaxf(v, __shfl_xor(v, 32));
-  return v;
+  return xrow_max(v);
 }
 __device__ __forceinline__ float rowpair_sum(float v) {
-  v += __shfl_xor(v, 8);
-  v += __shfl_xor(v, 16);
-  v += __shfl_xor(v, 32);
-  return v;
+  v += dpp<0x128>(v);  // row_ror:8 -- lane l ^ 8 within its 16-lane row
+  return xrow_sum(v);
 }
 
 // Per-head RMSNorm then RoPE (model/layers.py:18-22, 56-65 rounding) of the 16 dims this lane holds

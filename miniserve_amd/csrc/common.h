@@ -99,17 +99,30 @@ __device__ __forceinline__ float row16_max(float v) {
   v = fmaxf(v, dpp<0x140>(v));
   return v;
 }
+// v[l] + v[l ^ 16] and v[l] + v[l ^ 32] (and the maxima) on gfx950's row swaps:
+// v_permlane16_swap_b32 with both operands v leaves the even rows' values in one result and the
+// odd rows' in the other, in every lane; v_permlane32_swap does the same for the two halves. VALU
+// only -- no LDS round trip as with ds_bpermute. The same sums, bit for bit, as adding the
+// xor-shuffled value (the additions commute).
+__device__ __forceinline__ float xor16_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor16_max(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
 // Across the four 16-lane rows of a wavefront (lanes l, l^16, l^32, l^48).
-__device__ __forceinline__ float xrow_sum(float v) {
-  v += __shfl_xor(v, 16);
-  v += __shfl_xor(v, 32);
-  return v;
-}
-__device__ __forceinline__ float xrow_max(float v) {
-  v = fmaxf(v, __shfl_xor(v, 16));
-  v = fmaxf(v, __shfl_xor(v, 32));
-  return v;
-}
+__device__ __forceinline__ float xrow_sum(float v) { return xor32_sum(xor16_sum(v)); }
+__device__ __forceinline__ float xrow_max(float v) { return xor32_max(xor16_max(v)); }
 __device__ __forceinline__ float wave_sum(float v) { return xrow_sum(row16_sum(v)); }
 __device__ __forceinline__ float wave_max(float v) { return xrow_max(row16_max(v)); }
 

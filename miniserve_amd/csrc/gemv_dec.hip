@@ -214,8 +214,7 @@ __global__ __launch_bounds__(64 * KW) __attribute__((amdgpu_waves_per_eu(1, 1)))
           s = dot2_bf16(xa[mt][c][h].z, xa[mt][c][h].z, s);
           s = dot2_bf16(xa[mt][c][h].w, xa[mt][c][h].w, s);
         }
-      s += __shfl_xor(s, 16);
-      s += __shfl_xor(s, 32);
+      s = xrow_sum(s);
       ss[mt] = s;
     }
     if (g == 0) {

@@ -147,8 +147,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void dec_stream_kernel(StreamArg
         s = dot2_bf16(xa[c][h].z, xa[c][h].z, s);
         s = dot2_bf16(xa[c][h].w, xa[c][h].w, s);
       }
-    s += __shfl_xor(s, 16);
-    s += __shfl_xor(s, 32);
+    s = xrow_sum(s);
     if (g == 0) s_ss[ks][j] = s;
     __syncthreads();  // every wavefront's partial sums of squares
     float tot = 0.f;
