@@ -298,10 +298,14 @@ int msa_sampling_probs(const float* logits, int64_t ld, int64_t rows, int64_t vo
 /* sample (runner/sampler.py:55-69): out_ids[r] = argmax(logits[r]) (first index) where
  * greedy[r] != 0, else the exponential race argmax_i probs[r][i] / max(noise[r][i], FLT_MIN) with
  * probs as msa_sampling_probs and noise ~ Exp(1) [rows, ldn] drawn by the caller (the reference
- * draws it with torch's exponential_, per-row generators for seeded requests). */
+ * draws it with torch's exponential_, per-row generators for seeded requests). With a workspace
+ * of msa_sample_workspace_size(rows, vocab) bytes (rows <= 65535), greedy rows and rows with
+ * 0 < top_k <= 256 are spread over vocabulary chunks (two launches); a NULL workspace takes one
+ * workgroup per row. */
+size_t msa_sample_workspace_size(int64_t rows, int64_t vocab);
 int msa_sample(const float* logits, int64_t ld, int64_t rows, int64_t vocab, const float* temperature,
                const int32_t* top_k, const float* top_p, const uint8_t* greedy, const float* noise, int64_t ldn,
-               int64_t* out_ids, msa_stream_t stream);
+               int64_t* out_ids, void* workspace, size_t workspace_bytes, msa_stream_t stream);
 
 /* ---- speculative-decoding verification (spec/rejection.py) ----------------------------------- */
 

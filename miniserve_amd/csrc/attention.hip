@@ -728,10 +728,13 @@ constexpr int kDecodeWideTokens = 1024;
 template <int G, bool QKV = false>
 static void launch_decode(const DecodeArgs& a, int num_seqs, hipStream_t s) {
   const dim3 grid(a.kv_heads, a.splits, num_seqs);
-  if (!QKV && G <= 2 && a.part_tokens >= kDecodeWideTokens)
-    hipLaunchKernelGGL((paged_decode_kernel<G, 2 * kDecodeW, QKV>), grid, dim3(128 * kDecodeW), 0, s, a);
-  else
-    hipLaunchKernelGGL((paged_decode_kernel<G, kDecodeW, QKV>), grid, dim3(64 * kDecodeW), 0, s, a);
+  if constexpr (!QKV && G <= 2) {  // (no eight-wavefront instantiation where it is never launched)
+    if (a.part_tokens >= kDecodeWideTokens) {
+      hipLaunchKernelGGL((paged_decode_kernel<G, 2 * kDecodeW, QKV>), grid, dim3(128 * kDecodeW), 0, s, a);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((paged_decode_kernel<G, kDecodeW, QKV>), grid, dim3(64 * kDecodeW), 0, s, a);
 }
 
 // Shared checks and workspace binding of the two decode entry points.

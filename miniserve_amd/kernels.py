@@ -688,11 +688,16 @@ def sample_ids(
     _check(noise.dtype == torch.float32 and noise.dim() == 2 and noise.shape == (r, v) and noise.stride(-1) == 1,
            "sample_ids: noise [R, V] float32")
     out = torch.empty(r, dtype=torch.int64, device=logits.device)
-    _native.call("msa_sample", _ptr(logits), logits.stride(0), r, v,
-                 _ptr(_opt_param(temperature, torch.float32, r, "temperature")),
-                 _ptr(_opt_param(top_k, torch.int32, r, "top_k")), _ptr(_opt_param(top_p, torch.float32, r, "top_p")),
-                 _ptr(_opt_param(greedy, torch.uint8, r, "greedy")), _ptr(noise), noise.stride(0), _ptr(out),
-                 _stream(logits))
+    temps = _opt_param(temperature, torch.float32, r, "temperature")
+    tk = _opt_param(top_k, torch.int32, r, "top_k")
+    tp = _opt_param(top_p, torch.float32, r, "top_p")
+    gr = _opt_param(greedy, torch.uint8, r, "greedy")
+    # Greedy rows and rows with 0 < top_k <= 256 run over vocabulary chunks (the workspace holds
+    # each chunk's candidates); the others fall back to a workgroup per row inside the same call.
+    ws_bytes = _native.query("msa_sample_workspace_size", r, v)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=logits.device) if ws_bytes else None
+    _native.call("msa_sample", _ptr(logits), logits.stride(0), r, v, _ptr(temps), _ptr(tk), _ptr(tp), _ptr(gr),
+                 _ptr(noise), noise.stride(0), _ptr(out), _ptr(ws), ws_bytes, _stream(logits))
     return out
 
 

@@ -150,3 +150,59 @@ def test_edge_rows():
     assert torch.equal(got[2] > float("-inf"), ref[2] > float("-inf"))
     mask, ok = brute_force_mask(x[3].double().numpy(), vocab, 0.999)
     assert not ok or np.array_equal((got[3] > float("-inf")).numpy(), mask)
+
+
+def _whole_row_ids(logits, temps, k, p, greedy, noise):
+    """msa_sample without a workspace: one workgroup per row over the whole vocabulary."""
+    from miniserve_amd import _native
+
+    r, v = logits.shape
+    out = torch.empty(r, dtype=torch.int64, device=DEV)
+    _native.call("msa_sample", logits.data_ptr(), logits.stride(0), r, v, temps.data_ptr(), k.data_ptr(),
+                 p.data_ptr(), greedy.data_ptr(), noise.data_ptr(), noise.stride(0), out.data_ptr(), None, 0,
+                 torch.cuda.current_stream().cuda_stream)
+    return out
+
+
+@pytest.mark.parametrize("vocab", [151936, 10240, 10241, 70000, 200000, 400000])
+def test_chunked_sampling_matches_the_whole_row_path(vocab):
+    """The chunked path (greedy rows and 0 < top_k <= 256 over vocabulary chunks) against the
+    whole-row path on the same logits and noise: identical ids wherever the best two scores differ
+    by more than 1e-5 relative (they sum Z in different orders). Rows: greedy, top-k 1..256 with
+    and without top-p, top-k above 256 and none (whole-row fallback inside the call), and rows of
+    rounded logits whose ties at the k-th value overflow a chunk's candidates (fallback) or fill
+    the finishing workgroup's bound (the radix path). Vocabularies: one chunk, a ragged last chunk,
+    up to 16 chunks and up to 32 (candidates gathered in registers), 40 (gathered through LDS)."""
+    rows = 48
+    g = torch.Generator().manual_seed(vocab)
+    logits = torch.randn(rows, vocab, generator=g) * 3
+    logits[40:] = torch.round(logits[40:])  # many equal values: ties at the cut
+    k = torch.randint(1, 257, (rows,), generator=g).to(torch.int32)
+    k[5] = 1
+    k[6] = 256
+    k[7] = 300  # above the chunked range
+    k[8] = vocab  # no top-k
+    p = (torch.rand(rows, generator=g) * 0.9 + 0.05).float()
+    p[::3] = 1.0
+    temps = (torch.rand(rows, generator=g) * 1.2 + 0.3).float()
+    greedy = torch.zeros(rows, dtype=torch.uint8)
+    greedy[::11] = 1
+    noise = torch.empty(rows, vocab).exponential_(generator=g)
+    ld, td, kd, pd, gd, nd = (t.to(DEV) for t in (logits, temps, k, p, greedy, noise))
+    got = kernels.sample_ids(ld, td, kd, pd, gd, nd).cpu()
+    whole = _whole_row_ids(ld, td, kd, pd, gd, nd).cpu()
+    again = kernels.sample_ids(ld, td, kd, pd, gd, nd).cpu()
+    assert torch.equal(got, again)  # deterministic
+    probs = osm.compute_probs(logits, temps, k.long(), p)
+    checked = 0
+    for r in range(rows):
+        if greedy[r]:
+            assert int(got[r]) == int(logits[r].argmax()), r
+            checked += 1
+            continue
+        s = (probs[r] / noise[r].clamp_min(1.17549435e-38)).double()
+        top2 = s.topk(2).values
+        if float(top2[0] - top2[1]) > 1e-5 * float(top2[0]):
+            assert int(got[r]) == int(whole[r]), r
+            checked += 1
+    assert checked >= rows * 3 // 4
