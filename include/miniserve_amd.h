@@ -148,6 +148,20 @@ int msa_lm_head_argmax(const uint16_t* hidden, int64_t ld_hidden, int64_t hidden
                        const uint16_t* norm_w, float eps, const uint16_t* weight, int64_t vocab, int64_t* out_ids,
                        void* workspace, size_t workspace_bytes, msa_stream_t stream);
 
+/* Bytes of workspace msa_lm_head_logits needs (the normalized rows of the GEMM route; 0 when the
+ * rows take the streaming route). */
+size_t msa_lm_head_logits_workspace_size(int64_t num_rows, int64_t k, int64_t vocab);
+
+/* Final norm + LM head for the sampled rows (model/qwen3.py:152-158 with the row selection of
+ * runner/model_runner.py:211): logits[i][v] = float(bf16(RMSNorm(hidden[rows[i]]) . weight[v]))
+ * for i < num_rows, v < vocab -- compute_logits' bf16 product cast to float32 -- into logits
+ * [num_rows, ld_logits] (ld_logits >= vocab). norm_w NULL: the rows are taken as already
+ * normalized. Shapes, routes and alignment as msa_lm_head_argmax. */
+int msa_lm_head_logits(const uint16_t* hidden, int64_t ld_hidden, int64_t hidden_rows, const int64_t* rows,
+                       int64_t num_rows, int64_t k, const uint16_t* norm_w, float eps, const uint16_t* weight,
+                       int64_t vocab, float* logits, int64_t ld_logits, void* workspace, size_t workspace_bytes,
+                       msa_stream_t stream);
+
 /* ---- norms, RoPE and the KV-cache write (model/layers.py, model/qwen3.py) -------------------- */
 
 /* RMSNorm.forward (model/layers.py:18-22): out = bf16(w * bf16(x * rsqrt(mean(x^2) + eps))). */

@@ -16,7 +16,7 @@ from pathlib import Path
 import torch  # noqa: F401  -- must be imported before the HIP library is loaded
 
 LIB_PATH = Path(__file__).resolve().parent / "libminiserve_amd.so"
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 # name -> (restype, argtypes); mirrors include/miniserve_amd.h.
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
@@ -83,6 +83,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         c_int,
         [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_float, c_void_p, c_int64, c_void_p,
          c_void_p, c_size_t, c_void_p],
+    ),
+    "msa_lm_head_logits_workspace_size": (c_size_t, [c_int64, c_int64, c_int64]),
+    "msa_lm_head_logits": (
+        c_int,
+        [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_float, c_void_p, c_int64, c_void_p,
+         c_int64, c_void_p, c_size_t, c_void_p],
     ),
     "msa_top_k_top_p_mask": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_int64, c_void_p]),
     "msa_sampling_probs": (

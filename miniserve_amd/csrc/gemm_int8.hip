@@ -358,13 +358,17 @@ struct LmGemmArgs {
   const uint16_t* w;  // [n, k] bf16
   float* cand_val;    // [m, n_blocks]
   int32_t* cand_idx;  // [m, n_blocks]
+  float* logits;      // [m, ldl] (the logits route)
+  int64_t ldl;
   int m, n, k;
   int n_blocks, m_blocks;
 };
 
 // Workgroup b: XCD b % 8 takes vocabulary blocks nb = xcd (mod 8) and runs the row blocks of each
-// such nb back to back, so repeated weight tiles come from that XCD's L2.
-__global__ __launch_bounds__(256) void lm_gemm_argmax_kernel(LmGemmArgs a) {
+// such nb back to back, so repeated weight tiles come from that XCD's L2. LOGITS: the bf16-rounded
+// logits are written out as float32 instead of the argmax candidates.
+template <bool LOGITS>
+__global__ __launch_bounds__(256) void lm_gemm_kernel(LmGemmArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint16_t gsm[];
   const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
   const int nb = (slot / a.m_blocks) * 8 + xcd, mb = slot % a.m_blocks;
@@ -450,6 +454,21 @@ __global__ __launch_bounds__(256) void lm_gemm_argmax_kernel(LmGemmArgs a) {
 #undef MSA_LM_STORE
 
   // lane (g, j) of tile (mt, nt): row wm*64 + mt*16 + 4g + i, vocabulary entry n0 + wn*64 + nt*16 + j.
+  if constexpr (LOGITS) {
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = m0 + wm * 64 + mt * 16 + 4 * g + i;
+        if (r >= a.m) continue;
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) {
+          const int col = n0 + wn * 64 + nt * 16 + j;
+          if (col < a.n) a.logits[(int64_t)r * a.ldl + col] = round_bf16(acc[mt][nt][i]);
+        }
+      }
+    return;
+  }
   // Per row: the lane's best over nt (increasing entries), then over the 16 lanes j, then over wn.
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
@@ -496,29 +515,31 @@ __global__ __launch_bounds__(256) void lm_gemm_argmax_kernel(LmGemmArgs a) {
 int lm_gemm_vocab_blocks(int64_t vocab) { return (int)((vocab + kGBN - 1) / kGBN); }
 
 // Gather + norm into `xn` ([num_rows, k] bf16), then the GEMM writes [num_rows][n_blocks]
-// candidates. k % 64 == 0.
-int launch_lm_gemm_argmax(const uint16_t* hidden, int64_t ld_hidden, int64_t hidden_rows, const int64_t* rows,
-                          int num_rows, int k, const uint16_t* norm_w, float eps, const uint16_t* weight, int vocab,
-                          uint16_t* xn, float* cand_val, int32_t* cand_idx, hipStream_t s) {
+// candidates, or the logits [num_rows][ldl] when `logits` is set. k % 64 == 0.
+int launch_lm_gemm(const uint16_t* hidden, int64_t ld_hidden, int64_t hidden_rows, const int64_t* rows, int num_rows,
+                   int k, const uint16_t* norm_w, float eps, const uint16_t* weight, int vocab, uint16_t* xn,
+                   float* cand_val, int32_t* cand_idx, float* logits, int64_t ldl, hipStream_t s) {
   hipLaunchKernelGGL(lm_rows_prologue_kernel, dim3(num_rows), dim3(256), 0, s, hidden, ld_hidden, hidden_rows, rows,
                      norm_w, eps, k, xn);
-  int rc = check_launch("msa_lm_head_argmax (row prologue)");
+  int rc = check_launch("LM head (row prologue)");
   if (rc != MSA_OK) return rc;
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)lm_gemm_argmax_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)kGemmLds);
-    if (e != hipSuccess) return fail(MSA_ERR_LAUNCH, std::string("hipFuncSetAttribute: ") + hipGetErrorString(e));
+    for (const void* f : {(const void*)lm_gemm_kernel<false>, (const void*)lm_gemm_kernel<true>}) {
+      hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemmLds);
+      if (e != hipSuccess) return fail(MSA_ERR_LAUNCH, std::string("hipFuncSetAttribute: ") + hipGetErrorString(e));
+    }
     attr_set = true;
   }
   LmGemmArgs a{};
-  a.x = xn; a.w = weight; a.cand_val = cand_val; a.cand_idx = cand_idx;
+  a.x = xn; a.w = weight; a.cand_val = cand_val; a.cand_idx = cand_idx; a.logits = logits; a.ldl = ldl;
   a.m = num_rows; a.n = vocab; a.k = k;
   a.n_blocks = lm_gemm_vocab_blocks(vocab);
   a.m_blocks = (num_rows + kGBM - 1) / kGBM;
   const int blocks = ((a.n_blocks + 7) / 8) * 8 * a.m_blocks;
-  hipLaunchKernelGGL(lm_gemm_argmax_kernel, dim3(blocks), dim3(256), kGemmLds, s, a);
-  return check_launch("msa_lm_head_argmax (GEMM)");
+  if (logits) hipLaunchKernelGGL(lm_gemm_kernel<true>, dim3(blocks), dim3(256), kGemmLds, s, a);
+  else hipLaunchKernelGGL(lm_gemm_kernel<false>, dim3(blocks), dim3(256), kGemmLds, s, a);
+  return check_launch("LM head (GEMM)");
 }
 
 }  // namespace msa

@@ -82,6 +82,9 @@ struct RowsArgs {
   // argmax candidates [t][n_rb]
   float* cand_val;
   int32_t* cand_idx;
+  // LM-head logits [t][ldl] float32 (the logits route)
+  float* logits;
+  int64_t ldl;
 };
 
 
@@ -472,15 +475,16 @@ __global__ __launch_bounds__(64 * RT * KW) void int8_rows_kernel(RowsArgs a) {
   }
 }
 
-// bf16 LM head + greedy argmax, persistent over vocabulary row tiles. A workgroup (W waves)
-// stages up to 64 sampled rows, normalized once, in LDS ([64][K + 8] bf16), then its waves take
-// 16-row tiles of the weight round-robin (tiles wg * W + wave, + W * gridDim, ...). Per tile a
-// lane streams its row's K in 32-wide chunks (one 16-byte bf16 load per chunk, PF chunks in
-// flight), multiplies on MFMA against the MT token tiles, rounds each logit to bf16 (the
-// reference's logits dtype) and keeps a running (max, first index) per token. The waves then meet
-// in LDS and write one candidate per (workgroup, token); argmax_candidates_kernel picks the winner.
-template <int W, int MT, int PRO, int PF>
-__global__ __launch_bounds__(64 * W) void lm_head_argmax_kernel(RowsArgs a) {
+// bf16 LM head, persistent over vocabulary row tiles. A workgroup (W waves) stages up to 64
+// sampled rows, normalized once, in LDS ([64][K + 8] bf16), then its waves take 16-row tiles of
+// the weight round-robin (tiles wg * W + wave, + W * gridDim, ...). Per tile a lane streams its
+// row's K in 32-wide chunks (one 16-byte bf16 load per chunk, PF chunks in flight), multiplies on
+// MFMA against the MT token tiles and rounds each logit to bf16 (the reference's logits dtype).
+// LOGITS: the logits are written out as float32. Otherwise (greedy rows) each lane keeps a running
+// (max, first index) per token; the waves then meet in LDS and write one candidate per
+// (workgroup, token), and argmax_candidates_kernel picks the winner.
+template <int W, int MT, int PRO, int PF, bool LOGITS>
+__global__ __launch_bounds__(64 * W) void lm_head_kernel(RowsArgs a) {
   constexpr int CH = 32;  // K per chunk (bf16: 16 bytes per lane)
   constexpr int NTH = 64 * W;
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
@@ -575,17 +579,30 @@ __global__ __launch_bounds__(64 * W) void lm_head_argmax_kernel(RowsArgs a) {
     }
     }
     // lane (g, j) holds logits of tokens mt*16 + 4g + i for vocabulary row `row`
+    if constexpr (LOGITS) {
+      if (row < a.n) {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float v = row < a.n ? round_bf16(acc[mt][i]) : -INFINITY;
-        if (v > best[mt][i]) {  // rows arrive in increasing order per lane: ties keep the first
-          best[mt][i] = v;
-          bidx[mt][i] = row;
-        }
+          for (int i = 0; i < 4; ++i) {
+            const int t = mt * 16 + 4 * g + i;
+            if (t < a.t) a.logits[(int64_t)t * a.ldl + row] = round_bf16(acc[mt][i]);
+          }
       }
+    } else {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float v = row < a.n ? round_bf16(acc[mt][i]) : -INFINITY;
+          if (v > best[mt][i]) {  // rows arrive in increasing order per lane: ties keep the first
+            best[mt][i] = v;
+            bidx[mt][i] = row;
+          }
+        }
+    }
   }
+  if constexpr (LOGITS) return;
   // Reduce over the 16 lanes j (rows), then over the waves through LDS.
   float* cv = (float*)(smem + MT * 16 * ldsx);  // [W][64]
   int32_t* ci = (int32_t*)(cv + W * 64);        // [W][64]
@@ -826,9 +843,9 @@ constexpr int kLmW = 8;         // wavefronts per LM-head workgroup
 
 namespace msa {  // the GEMM route of the LM head (gemm_int8.hip)
 int lm_gemm_vocab_blocks(int64_t vocab);
-int launch_lm_gemm_argmax(const uint16_t* hidden, int64_t ld_hidden, int64_t hidden_rows, const int64_t* rows,
-                          int num_rows, int k, const uint16_t* norm_w, float eps, const uint16_t* weight, int vocab,
-                          uint16_t* xn, float* cand_val, int32_t* cand_idx, hipStream_t s);
+int launch_lm_gemm(const uint16_t* hidden, int64_t ld_hidden, int64_t hidden_rows, const int64_t* rows, int num_rows,
+                   int k, const uint16_t* norm_w, float eps, const uint16_t* weight, int vocab, uint16_t* xn,
+                   float* cand_val, int32_t* cand_idx, float* logits, int64_t ldl, hipStream_t s);
 }  // namespace msa
 
 // 16-row activation tiles one streaming launch holds in LDS (0: not even one).
@@ -854,41 +871,50 @@ extern "C" size_t msa_lm_head_argmax_workspace_size(int64_t num_rows, int64_t k,
   return (size_t)num_rows * kLmBlocks * (sizeof(float) + sizeof(int32_t));
 }
 
-extern "C" int msa_lm_head_argmax(const uint16_t* hidden, int64_t ld_hidden, int64_t hidden_rows, const int64_t* rows,
-                                  int64_t num_rows, int64_t k, const uint16_t* norm_w, float eps,
-                                  const uint16_t* weight, int64_t vocab, int64_t* out_ids, void* workspace,
-                                  size_t workspace_bytes, msa_stream_t stream) {
+extern "C" size_t msa_lm_head_logits_workspace_size(int64_t num_rows, int64_t k, int64_t vocab) {
+  if (num_rows <= 0 || vocab <= 0 || k <= 0) return 0;
+  return lm_use_gemm(num_rows, k) ? align256((size_t)num_rows * k * 2) : 0;
+}
+
+// The LM head over num_rows gathered rows: greedy ids (logits == nullptr) or float32 logits.
+static int lm_head_run(const char* name, const uint16_t* hidden, int64_t ld_hidden, int64_t hidden_rows,
+                       const int64_t* rows, int64_t num_rows, int64_t k, const uint16_t* norm_w, float eps,
+                       const uint16_t* weight, int64_t vocab, int64_t* out_ids, float* logits, int64_t ldl,
+                       void* workspace, size_t workspace_bytes, msa_stream_t stream) {
+  const std::string nm(name);
   if (num_rows == 0) return MSA_OK;
-  if (!hidden || !rows || !weight || !out_ids) return fail(MSA_ERR_INVALID, "msa_lm_head_argmax: null pointer");
-  if (num_rows < 0 || num_rows > 0x7fffffff || vocab <= 0 || vocab > 0x7fffffff || k <= 0 || hidden_rows <= 0)
-    return fail(MSA_ERR_INVALID, "msa_lm_head_argmax: bad shape");
-  if (k % 32 != 0) return fail(MSA_ERR_UNSUPPORTED, "msa_lm_head_argmax: hidden must be a multiple of 32");
+  if (!hidden || !rows || !weight || (!out_ids && !logits)) return fail(MSA_ERR_INVALID, nm + ": null pointer");
+  if (num_rows < 0 || num_rows > 0x7fffffff || vocab <= 0 || vocab > 0x7fffffff || k <= 0 || hidden_rows <= 0 ||
+      (logits && ldl < vocab))
+    return fail(MSA_ERR_INVALID, nm + ": bad shape");
+  if (k % 32 != 0) return fail(MSA_ERR_UNSUPPORTED, nm + ": hidden must be a multiple of 32");
   if (ld_hidden < k || ld_hidden % 8 != 0 || !aligned16(hidden) || !aligned16(weight) || (norm_w && !aligned16(norm_w)))
-    return fail(MSA_ERR_INVALID, "msa_lm_head_argmax: hidden / weight / norm_w must be 16-byte aligned");
-  const size_t need = msa_lm_head_argmax_workspace_size(num_rows, k, vocab);
-  if (!workspace || workspace_bytes < need) return fail(MSA_ERR_WORKSPACE, "msa_lm_head_argmax: workspace too small");
-  if (!aligned16(workspace)) return fail(MSA_ERR_INVALID, "msa_lm_head_argmax: workspace must be 16-byte aligned");
+    return fail(MSA_ERR_INVALID, nm + ": hidden / weight / norm_w must be 16-byte aligned");
+  const size_t need = logits ? msa_lm_head_logits_workspace_size(num_rows, k, vocab)
+                             : msa_lm_head_argmax_workspace_size(num_rows, k, vocab);
+  if (need > 0 && (!workspace || workspace_bytes < need)) return fail(MSA_ERR_WORKSPACE, nm + ": workspace too small");
+  if (need > 0 && !aligned16(workspace)) return fail(MSA_ERR_INVALID, nm + ": workspace must be 16-byte aligned");
   hipStream_t s = (hipStream_t)stream;
   if (lm_use_gemm(num_rows, k)) {
     uint16_t* xn = (uint16_t*)workspace;
     const int nbk = lm_gemm_vocab_blocks(vocab);
-    float* gval = (float*)((char*)workspace + align256((size_t)num_rows * k * 2));
-    int32_t* gidx = (int32_t*)(gval + (size_t)num_rows * nbk);
-    const int rc = launch_lm_gemm_argmax(hidden, ld_hidden, hidden_rows, rows, (int)num_rows, (int)k, norm_w, eps, weight,
-                                         (int)vocab, xn, gval, gidx, s);
-    if (rc != MSA_OK) return rc;
+    float* gval = logits ? nullptr : (float*)((char*)workspace + align256((size_t)num_rows * k * 2));
+    int32_t* gidx = logits ? nullptr : (int32_t*)(gval + (size_t)num_rows * nbk);
+    const int rc = launch_lm_gemm(hidden, ld_hidden, hidden_rows, rows, (int)num_rows, (int)k, norm_w, eps, weight,
+                                  (int)vocab, xn, gval, gidx, logits, ldl, s);
+    if (rc != MSA_OK || logits) return rc;
     hipLaunchKernelGGL(argmax_candidates_kernel, dim3((unsigned)num_rows), dim3(256), 0, s, gval, gidx, nbk, out_ids);
-    return check_launch("msa_lm_head_argmax (candidates)");
+    return check_launch((nm + " (candidates)").c_str());
   }
   const int64_t nch = k / 32;  // 32-wide K chunks per vocabulary row; the load ring depth divides it
-  float* cand_val = (float*)workspace;
-  int32_t* cand_idx = (int32_t*)((char*)workspace + (size_t)num_rows * kLmBlocks * sizeof(float));
+  float* cand_val = logits ? nullptr : (float*)workspace;
+  int32_t* cand_idx = logits ? nullptr : (int32_t*)((char*)workspace + (size_t)num_rows * kLmBlocks * sizeof(float));
   // Launches of up to 64 rows each (fewer when 16-row activation tiles of this width fill LDS);
-  // every launch writes its rows' candidates. Each launch streams the whole weight once.
+  // every launch writes its rows' candidates or logits. Each launch streams the whole weight once.
   constexpr int W = kLmW;
   const size_t tile_bytes = (size_t)16 * (k + 8) * 2;
   const int64_t max_mt = lm_tiles_per_launch(k);
-  if (max_mt < 1) return fail(MSA_ERR_UNSUPPORTED, "msa_lm_head_argmax: hidden too large for the LDS activation tile");
+  if (max_mt < 1) return fail(MSA_ERR_UNSUPPORTED, nm + ": hidden too large for the LDS activation tile");
   for (int64_t r0 = 0; r0 < num_rows; r0 += 16 * max_mt) {
     const int nr = (int)std::min<int64_t>(16 * max_mt, num_rows - r0);
     const int mt = (nr + 15) / 16;
@@ -896,16 +922,24 @@ extern "C" int msa_lm_head_argmax(const uint16_t* hidden, int64_t ld_hidden, int
     RowsArgs a{};
     a.x = hidden; a.ldx = ld_hidden; a.x_rows = hidden_rows; a.gather = rows + r0; a.norm_w = norm_w; a.eps = eps;
     a.t = nr; a.k = (int)k; a.w = weight; a.n = (int)vocab;
-    a.cand_val = cand_val + r0 * kLmBlocks;
-    a.cand_idx = cand_idx + r0 * kLmBlocks;
+    if (logits) {
+      a.logits = logits + r0 * ldl;
+      a.ldl = ldl;
+    } else {
+      a.cand_val = cand_val + r0 * kLmBlocks;
+      a.cand_idx = cand_idx + r0 * kLmBlocks;
+    }
     int rc;
-#define MSA_LM_LAUNCH_PF(MT, PF)                                                                                     \
-  rc = norm_w ? launch_rows(lm_head_argmax_kernel<W, MT, RB_PRO_GATHER_RMSNORM, PF>, 64 * W, lds, kLmBlocks, a, s) \
-              : launch_rows(lm_head_argmax_kernel<W, MT, RB_PRO_GATHER, PF>, 64 * W, lds, kLmBlocks, a, s)
+#define MSA_LM_LAUNCH_L(MT, PF, L)                                                                                     \
+  rc = norm_w ? launch_rows(lm_head_kernel<W, MT, RB_PRO_GATHER_RMSNORM, PF, L>, 64 * W, lds, kLmBlocks, a, s) \
+              : launch_rows(lm_head_kernel<W, MT, RB_PRO_GATHER, PF, L>, 64 * W, lds, kLmBlocks, a, s)
+#define MSA_LM_LAUNCH_PF(MT, PF)       \
+  if (logits) MSA_LM_LAUNCH_L(MT, PF, true); \
+  else MSA_LM_LAUNCH_L(MT, PF, false);
 #define MSA_LM_LAUNCH(MT)                                  \
-  if (nch % 32 == 0) MSA_LM_LAUNCH_PF(MT, 16);             \
-  else if (nch % 8 == 0) MSA_LM_LAUNCH_PF(MT, 4);          \
-  else MSA_LM_LAUNCH_PF(MT, 1);
+  if (nch % 32 == 0) { MSA_LM_LAUNCH_PF(MT, 16) }          \
+  else if (nch % 8 == 0) { MSA_LM_LAUNCH_PF(MT, 4) }       \
+  else { MSA_LM_LAUNCH_PF(MT, 1) }
     switch (mt) {
       case 1: MSA_LM_LAUNCH(1); break;
       case 2: MSA_LM_LAUNCH(2); break;
@@ -914,11 +948,31 @@ extern "C" int msa_lm_head_argmax(const uint16_t* hidden, int64_t ld_hidden, int
     }
 #undef MSA_LM_LAUNCH
 #undef MSA_LM_LAUNCH_PF
+#undef MSA_LM_LAUNCH_L
     if (rc != MSA_OK) return rc;
-    rc = check_launch("msa_lm_head_argmax");
+    rc = check_launch(nm.c_str());
     if (rc != MSA_OK) return rc;
   }
+  if (logits) return MSA_OK;
   hipLaunchKernelGGL(argmax_candidates_kernel, dim3((unsigned)num_rows), dim3(256), 0, s, cand_val, cand_idx,
                      kLmBlocks, out_ids);
-  return check_launch("msa_lm_head_argmax (candidates)");
+  return check_launch((nm + " (candidates)").c_str());
+}
+
+extern "C" int msa_lm_head_argmax(const uint16_t* hidden, int64_t ld_hidden, int64_t hidden_rows, const int64_t* rows,
+                                  int64_t num_rows, int64_t k, const uint16_t* norm_w, float eps,
+                                  const uint16_t* weight, int64_t vocab, int64_t* out_ids, void* workspace,
+                                  size_t workspace_bytes, msa_stream_t stream) {
+  if (num_rows > 0 && !out_ids) return fail(MSA_ERR_INVALID, "msa_lm_head_argmax: null pointer");
+  return lm_head_run("msa_lm_head_argmax", hidden, ld_hidden, hidden_rows, rows, num_rows, k, norm_w, eps, weight,
+                     vocab, out_ids, nullptr, 0, workspace, workspace_bytes, stream);
+}
+
+extern "C" int msa_lm_head_logits(const uint16_t* hidden, int64_t ld_hidden, int64_t hidden_rows, const int64_t* rows,
+                                  int64_t num_rows, int64_t k, const uint16_t* norm_w, float eps,
+                                  const uint16_t* weight, int64_t vocab, float* logits, int64_t ld_logits,
+                                  void* workspace, size_t workspace_bytes, msa_stream_t stream) {
+  if (num_rows > 0 && !logits) return fail(MSA_ERR_INVALID, "msa_lm_head_logits: null pointer");
+  return lm_head_run("msa_lm_head_logits", hidden, ld_hidden, hidden_rows, rows, num_rows, k, norm_w, eps, weight,
+                     vocab, nullptr, logits, ld_logits, workspace, workspace_bytes, stream);
 }

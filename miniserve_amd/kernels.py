@@ -628,6 +628,31 @@ def lm_head_argmax(
     return out
 
 
+def lm_head_logits(
+    hidden: Tensor, rows: Tensor, norm_w: Tensor | None, eps: float, weight: Tensor, prenormed: bool = False
+) -> Tensor:
+    """Logits of the sampled rows: float32(bf16(RMSNorm(hidden[rows]) @ weight^T)) -- the reference's
+    ``compute_logits`` on the final norm's rows (model/qwen3.py:152-158); float32 [R, vocab].
+    ``prenormed``: hidden already holds the final norm's output (no RMSNorm is applied)."""
+    _on_gpu(hidden, rows, weight)
+    _check(hidden.dtype == torch.bfloat16 and hidden.dim() == 2 and hidden.stride(-1) == 1, "lm_head_logits: hidden")
+    _check(rows.dtype == torch.int64 and rows.is_contiguous(), "lm_head_logits: rows must be int64")
+    _check(weight.dtype == torch.bfloat16 and weight.is_contiguous() and weight.shape[1] == hidden.shape[1],
+           "lm_head_logits: weight [vocab, hidden] bf16")
+    _check(prenormed or norm_w is not None, "lm_head_logits: norm_w required unless prenormed")
+    r = rows.numel()
+    vocab, k = weight.shape
+    out = torch.empty(r, vocab, dtype=torch.float32, device=hidden.device)
+    ws_bytes = _native.query("msa_lm_head_logits_workspace_size", r, k, vocab) if r else 0
+    ws = workspaces.get("lm_head", hidden.device, ws_bytes)
+    _native.call(
+        "msa_lm_head_logits", _ptr(hidden), hidden.stride(0), hidden.shape[0], _ptr(rows), r, k,
+        _ptr(None if prenormed else norm_w), float(eps), _ptr(weight), vocab, _ptr(out), out.stride(0),
+        _ptr(ws), ws.numel() if ws is not None else 0, _stream(hidden),
+    )
+    return out
+
+
 # ---- sampling ---------------------------------------------------------------------------------------
 
 
@@ -695,9 +720,10 @@ def sample_ids(
     # Greedy rows and rows with 0 < top_k <= 256 run over vocabulary chunks (the workspace holds
     # each chunk's candidates); the others fall back to a workgroup per row inside the same call.
     ws_bytes = _native.query("msa_sample_workspace_size", r, v)
-    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=logits.device) if ws_bytes else None
+    ws = workspaces.get("sample", logits.device, ws_bytes)
     _native.call("msa_sample", _ptr(logits), logits.stride(0), r, v, _ptr(temps), _ptr(tk), _ptr(tp), _ptr(gr),
-                 _ptr(noise), noise.stride(0), _ptr(out), _ptr(ws), ws_bytes, _stream(logits))
+                 _ptr(noise), noise.stride(0), _ptr(out), _ptr(ws), ws.numel() if ws is not None else 0,
+                 _stream(logits))
     return out
 
 

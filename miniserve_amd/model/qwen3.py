@@ -333,6 +333,31 @@ class Qwen3ForCausalLM(nn.Module):
                                                cfg.rms_norm_eps if nxt is self.norm else nxt.eps)
 
     def compute_logits(self, hidden: Tensor) -> Tensor:
-        """[n, hidden] -> [n, vocab] float32, the product in bf16 (qwen3.py:155-158)."""
+        """[n, hidden] -> [n, vocab] float32, the product in bf16 (qwen3.py:155-158). On the GPU the
+        HIP LM head (bf16 MFMA products rounded to bf16, as the reference's bf16 logits)."""
         weight = self.embed_tokens.weight if self.lm_head is None else self.lm_head.weight
-        return F.linear(hidden, weight).float()
+        if not hidden.is_cuda:
+            return F.linear(hidden, weight).float()
+        if hidden.shape[0] == 0:
+            return hidden.new_empty(0, weight.shape[0], dtype=torch.float32)
+        rows = torch.arange(hidden.shape[0], device=hidden.device)
+        return kernels.lm_head_logits(hidden.contiguous(), rows, None, 0.0, weight, prenormed=True)
+
+    def logits(
+        self,
+        input_ids: Tensor,
+        positions: Tensor,
+        kv_caches: list[tuple[Tensor, Tensor]],
+        meta: AttentionMetadata,
+        logits_rows: Tensor,
+    ) -> Tensor:
+        """``compute_logits(forward(...)[logits_rows])`` (runner/model_runner.py:208-211): on the
+        token-split path the final norm of the sampled rows runs inside the LM-head kernel."""
+        if len(kv_caches) != len(self.layers):
+            raise ValueError(f"{len(kv_caches)} KV caches for {len(self.layers)} layers")
+        if self._token_split_ok(input_ids.numel()) and logits_rows.numel() > 0:
+            weight = self.embed_tokens.weight if self.lm_head is None else self.lm_head.weight
+            residual = self._token_split_layers(input_ids, positions, kv_caches, meta)
+            return kernels.lm_head_logits(residual, logits_rows, self.norm.weight, self.norm.eps, weight)
+        hidden = self.forward(input_ids, positions, kv_caches, meta)
+        return self.compute_logits(hidden[logits_rows])

@@ -207,8 +207,8 @@ class ModelRunner:
 
     @torch.inference_mode()
     def forward_logits(self, inp: StepInputs) -> Tensor:
-        hidden = self.model(inp.input_ids, inp.positions, self.kv_caches, inp.attn)
-        return self.model.compute_logits(hidden[inp.logits_rows])
+        """Logits of the sampled rows (runner/model_runner.py:208-211)."""
+        return self.model.logits(inp.input_ids, inp.positions, self.kv_caches, inp.attn, inp.logits_rows)
 
     @torch.inference_mode()
     def forward_greedy(self, inp: StepInputs) -> Tensor:

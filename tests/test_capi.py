@@ -100,6 +100,11 @@ def test_workspace_sizes():
     assert _native.query("msa_lm_head_argmax_workspace_size", 65, 1024, 151936) == 65 * 1024 * 2 + 65 * 1187 * 8
     assert _native.query("msa_lm_head_argmax_workspace_size", 17, 4096, 151936) == 17 * 4096 * 2 + 17 * 1187 * 8
     assert _native.query("msa_lm_head_argmax_workspace_size", 16, 4096, 151936) == 16 * 256 * 8
+    assert _native.query("msa_lm_head_logits_workspace_size", 64, 1024, 151936) == 0  # streaming route
+    assert _native.query("msa_lm_head_logits_workspace_size", 65, 1024, 151936) == 65 * 1024 * 2  # normalized rows
+    # chunked sampling: 15 chunks of 10240 per 151936-entry row, 512 (key, index) pairs + 3 words each
+    assert _native.query("msa_sample_workspace_size", 64, 151936) == 64 * 15 * (512 * 8 + 12)
+    assert _native.query("msa_sample_workspace_size", 65536, 151936) == 0  # rows above the chunked path's limit
     assert _native.query("msa_paged_attention_decode_workspace_size", 64, 16, 128, 1) == 0
     ws = _native.query("msa_paged_attention_decode_workspace_size", 64, 16, 128, 8)
     assert ws >= 64 * 16 * 8 * (128 + 2) * 4

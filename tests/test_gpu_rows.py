@@ -212,6 +212,51 @@ def test_lm_head_argmax(rows, vocab, k):
     assert torch.equal(got, got2)
 
 
+# Streaming route: 1..64 rows per launch (16 at k = 4096; 70 rows at k = 96 take two launches);
+# GEMM route: more rows at k % 64 == 0.
+@pytest.mark.parametrize("rows,vocab,k", [(64, 151936, 1024), (5, 4099, 1024), (70, 3000, 96), (40, 9000, 4096),
+                                          (65, 20000, 1024), (200, 12000, 4096)])
+def test_lm_head_logits(rows, vocab, k):
+    """msa_lm_head_logits: each logit within one bf16 step (plus the float32 accumulation bound
+    2^-20 sum|h w|, which matters only where the sum cancels to near zero) of the float64 product of
+    the same bf16 operands rounded to bf16 (the reference's bf16 logits), rel-L2 against them 1e-3;
+    the argmax of the logits is exactly the id of msa_lm_head_argmax (the same products); prenormed
+    rows give the same logits."""
+    hidden, w, nw, sel = _lm_case(rows, vocab, k, seed=rows + vocab % 89)
+    hd, wd, nwd, seld = hidden.to(DEV), w.to(DEV), nw.to(DEV), sel.to(DEV)
+    got = kernels.lm_head_logits(hd, seld, nwd, 1e-6, wd).cpu()
+    assert got.shape == (rows, vocab) and got.dtype == torch.float32
+    h = ol.rms_norm(hidden[sel], nw, 1e-6)
+    ref = (h.double() @ w.double().T).to(torch.bfloat16).float()
+    assert torch.equal(got, got.to(torch.bfloat16).float())  # every value is a bf16 value
+    acc_err = (h.double().abs() @ w.double().abs().T).float() * 2.0**-20
+    assert bool(((got - ref).abs() <= (ref.abs() + acc_err) * 2.0**-7 + acc_err).all())
+    assert rel_l2(got, ref) < 1e-3
+    ids = kernels.lm_head_argmax(hd, seld, nwd, 1e-6, wd).cpu()
+    assert torch.equal(got.argmax(-1), ids)
+    got2 = kernels.lm_head_logits(h.to(DEV), torch.arange(rows).to(DEV), None, 0.0, wd, prenormed=True).cpu()
+    assert torch.equal(got, got2)
+
+
+def test_lm_head_logits_row_stride_and_clamped_rows():
+    """Through the C ABI: an output row stride above vocab leaves the padding untouched; row
+    indices outside [0, hidden_rows) are clamped (memory safety), as in msa_lm_head_argmax."""
+    from miniserve_amd import _native
+
+    rows, vocab, k, ld = 6, 1000, 256, 1031
+    hidden, w, nw, _ = _lm_case(rows, vocab, k, seed=3)
+    sel = torch.tensor([0, 8, -4, 2, 100, 5])
+    out = torch.full((rows, ld), 7.0, device=DEV)
+    hd, wd, nwd, seld = hidden.to(DEV), w.to(DEV), nw.to(DEV), sel.to(DEV)
+    _native.call("msa_lm_head_logits", hd.data_ptr(), k, hidden.shape[0], seld.data_ptr(), rows, k, nwd.data_ptr(),
+                 1e-6, wd.data_ptr(), vocab, out.data_ptr(), ld, None, 0, torch.cuda.current_stream().cuda_stream)
+    got = out.cpu()
+    assert bool((got[:, vocab:] == 7.0).all())
+    clamped = sel.clamp(0, hidden.shape[0] - 1)
+    want = kernels.lm_head_logits(hd, clamped.to(DEV), nwd, 1e-6, wd).cpu()
+    assert torch.equal(got[:, :vocab], want)
+
+
 @pytest.mark.parametrize("rows", [8, 100])  # the streaming route and the GEMM route
 def test_lm_head_argmax_first_index_wins_ties(rows):
     vocab, k = 20000, 1024
