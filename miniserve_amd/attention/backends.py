@@ -17,6 +17,7 @@ The metadata is built once per step and shared by all layers (backends.py:19-20)
 
 from __future__ import annotations
 
+import contextlib
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -144,17 +145,38 @@ def build_attention_metadata(chunks: list[SeqChunk], slot_mapping: Tensor, block
     return AttentionMetadata(slot_mapping, block_size, decode, prefill)
 
 
+_SIDE_STREAMS: dict[int, torch.cuda.Stream] = {}
+
+
+def _side_stream(device: torch.device) -> torch.cuda.Stream:
+    """A second stream per device (default priority) for the decode rows of a mixed batch."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    st = _SIDE_STREAMS.get(idx)
+    if st is None:
+        st = _SIDE_STREAMS[idx] = torch.cuda.Stream(device=idx)
+    return st
+
+
 def attend(q: Tensor, k_cache: Tensor, v_cache: Tensor, meta: AttentionMetadata, scale: float) -> Tensor:
     """Attention of every new token over its cached context (the caches already hold this
-    step's keys and values). q [T, H, D] -> [T, H, D]."""
+    step's keys and values). q [T, H, D] -> [T, H, D].
+
+    In a mixed batch the decode rows (HBM-bound) run on a second stream next to the prefill rows
+    (MFMA-bound); the two write disjoint rows of the output, and the caller's stream waits for both."""
     out = torch.empty_like(q)
     heads, kv_heads = q.shape[1], k_cache.shape[1]
+    side = None
+    if meta.decode is not None and meta.prefill is not None and q.is_cuda:
+        cur = torch.cuda.current_stream(q.device)
+        side = _side_stream(q.device)
+        side.wait_stream(cur)
     if meta.decode is not None:
         d = meta.decode
         ptok, parts = kernels.decode_splits(d.num_seqs, kv_heads, d.block_tables.shape[1], heads // kv_heads)
-        kernels.paged_attention_decode(
-            q, k_cache, v_cache, d.block_tables, d.context_lens, d.q_rows, ptok, parts, scale, out, meta.block_size
-        )
+        with torch.cuda.stream(side) if side is not None else contextlib.nullcontext():
+            kernels.paged_attention_decode(
+                q, k_cache, v_cache, d.block_tables, d.context_lens, d.q_rows, ptok, parts, scale, out, meta.block_size
+            )
     if meta.prefill is not None:
         p = meta.prefill
         group = heads // kv_heads
@@ -163,6 +185,8 @@ def attend(q: Tensor, k_cache: Tensor, v_cache: Tensor, meta: AttentionMetadata,
             raise RuntimeError(f"prefill attention supports H/KVH in 1, 2, 4 (got {group})")
         kernels.paged_attention_prefill(q, k_cache, v_cache, p.block_tables, p.seq_info, p.work[tile], scale, out,
                                         meta.block_size)
+    if side is not None:
+        torch.cuda.current_stream(q.device).wait_stream(side)
     return out
 
 
