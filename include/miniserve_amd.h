@@ -153,7 +153,7 @@ int msa_lm_head_argmax(const uint16_t* hidden, int64_t ld_hidden, int64_t hidden
 size_t msa_lm_head_logits_workspace_size(int64_t num_rows, int64_t k, int64_t vocab);
 
 /* Final norm + LM head for the sampled rows (model/qwen3.py:152-158 with the row selection of
- * runner/model_runner.py:211): logits[i][v] = float(bf16(RMSNorm(hidden[rows[i]]) . weight[v]))
+ * runner/model_runner.py:214-217): logits[i][v] = float(bf16(RMSNorm(hidden[rows[i]]) . weight[v]))
  * for i < num_rows, v < vocab -- compute_logits' bf16 product cast to float32 -- into logits
  * [num_rows, ld_logits] (ld_logits >= vocab). norm_w NULL: the rows are taken as already
  * normalized. Shapes, routes and alignment as msa_lm_head_argmax. */

@@ -351,7 +351,7 @@ class Qwen3ForCausalLM(nn.Module):
         meta: AttentionMetadata,
         logits_rows: Tensor,
     ) -> Tensor:
-        """``compute_logits(forward(...)[logits_rows])`` (runner/model_runner.py:208-211): on the
+        """``compute_logits(forward(...)[logits_rows])`` (runner/model_runner.py:214-217): on the
         token-split path the final norm of the sampled rows runs inside the LM-head kernel."""
         if len(kv_caches) != len(self.layers):
             raise ValueError(f"{len(kv_caches)} KV caches for {len(self.layers)} layers")

@@ -207,7 +207,7 @@ class ModelRunner:
 
     @torch.inference_mode()
     def forward_logits(self, inp: StepInputs) -> Tensor:
-        """Logits of the sampled rows (runner/model_runner.py:208-211)."""
+        """Logits of the sampled rows (runner/model_runner.py:214-217)."""
         return self.model.logits(inp.input_ids, inp.positions, self.kv_caches, inp.attn, inp.logits_rows)
 
     @torch.inference_mode()
