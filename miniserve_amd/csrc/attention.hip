@@ -10,12 +10,13 @@
 // workspace and a second small kernel merges them -- no workgroup ever waits for another.
 //
 // Prefill (any number of new tokens, fresh or after cached keys): flash-attention on MFMA. A
-// workgroup of four wavefronts owns one KV head and 64 / G query tokens; wavefront w takes query
-// head w % G and 16 of the tokens. Per 32-key tile the workgroup stages K (row-major) and V
-// (transposed) in LDS, then each wavefront computes S^T = K Q^T (v_mfma_f32_16x16x32_bf16, 2 x 4
-// instructions) so each lane holds 8 scores of ONE query, applies the causal mask and an online
-// softmax with lane-local statistics, and accumulates O^T += V^T P^T (8 instructions) with P in
-// bf16.
+// workgroup owns one KV head and 64 / G query tokens in two key groups of four wavefronts;
+// wavefront w of a group takes query head w % G and 16 of the tokens. Per 32-key tile a key group
+// stages K and V (both key-major) in LDS, then each wavefront computes S^T = K Q^T
+// (v_mfma_f32_16x16x32_bf16, 2 x 4 instructions) so each lane holds 8 scores of ONE query, applies
+// the causal mask and an online softmax with lane-local statistics, and accumulates
+// O^T += V^T P^T (8 instructions, V^T fragments through gfx950's transposing LDS reads) with P in
+// bf16; the softmax denominators accumulate on MFMA too (a ones matrix times P).
 #include <mutex>
 
 #include "common.h"
@@ -451,14 +452,18 @@ __global__ __launch_bounds__(kHeadDim) void paged_decode_reduce_kernel(DecodeArg
 
 // ---------------------------------------------------------------------------------------------
 
-constexpr int kKeyTile = 32;             // keys per LDS tile
-constexpr int kKsStride = kHeadDim + 8;  // bf16 elements per K row in LDS
-constexpr int kVtStride = kKeyTile + 4;  // bf16 elements per transposed V row in LDS
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;  // an LDS pointer for the transposing reads
+
+constexpr int kKeyTile = 32;              // keys per LDS tile
+constexpr int kKsStride = kHeadDim + 8;   // bf16 elements per K row in LDS
+constexpr int kVsStride = kHeadDim + 16;  // per V row: 288 bytes, so the 4 rows x 32 bytes a
+                                          // transposing read gathers per 16 lanes hit distinct banks
 constexpr int kKsTile = kKeyTile * kKsStride;
-constexpr int kVtTile = kHeadDim * kVtStride;
+constexpr int kVsTile = kKeyTile * kVsStride;
 constexpr int kKeyGroups = 2;  // groups of four wavefronts splitting a workgroup's key tiles
-// Per key group two buffers of K and V^T: 71,680 bytes, two workgroups per CU.
-constexpr size_t kPrefillLds = (size_t)kKeyGroups * 2 * (kKsTile + kVtTile) * 2;
+// Per key group two buffers of K and V (both key-major): 71,680 bytes, two workgroups per CU.
+constexpr size_t kPrefillLds = (size_t)kKeyGroups * 2 * (kKsTile + kVsTile) * 2;
 constexpr int kXchFloats = 34 * 64;  // per wavefront at the merge: 32 accumulators, m, l per lane
 static_assert((size_t)4 * kXchFloats * 4 <= kPrefillLds, "merge exchange fits the tile buffers");
 
@@ -480,7 +485,7 @@ struct PrefillArgs {
 };
 
 // Two key groups of four wavefronts: group kg takes key tiles kg, kg + 2, ... of the workgroup's
-// query tile, with its own double-buffered K / V^T tiles, and hands its softmax state to group 0
+// query tile, with its own double-buffered K / V tiles, and hands its softmax state to group 0
 // through LDS at the end -- twice the wavefronts in flight and half the chain of key tiles of the
 // longest query tile.
 template <int G>
@@ -490,8 +495,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
   extern __shared__ __attribute__((aligned(16))) uint16_t psm[];
   const int kg = __builtin_amdgcn_readfirstlane(threadIdx.x >> 8);  // key group
   const int tg = threadIdx.x & 255;                                  // thread within the key group
-  uint16_t* Ks = psm + kg * 2 * (kKsTile + kVtTile);  // [2][kKeyTile][kKsStride]
-  uint16_t* Vt = Ks + 2 * kKsTile;                     // [2][kHeadDim][kVtStride]
+  uint16_t* Ks = psm + kg * 2 * (kKsTile + kVsTile);  // [2][kKeyTile][kKsStride]
+  uint16_t* Vs = Ks + 2 * kKsTile;                     // [2][kKeyTile][kVsStride]
 
   const int wi = blockIdx.x, kvh = blockIdx.y;
   const int seq = a.work[2 * wi], tstart = a.work[2 * wi + 1];
@@ -522,65 +527,77 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
   const int64_t tok_stride = (int64_t)a.kv_heads * kHeadDim;
 
   // Loader role within the key group: keys 2la and 2la + 1 of the tile (both in block
-  // tile * 2 + la / 8), 8-wide dim chunk lb. A tile's table entry is read one tile before its keys
-  // and values, so the keys never wait on a table read; every load is issued unconditionally (the
-  // table index clamped into the row, a dead key's address masked to the cache's first row) and a
-  // dead key's value is zeroed where it is stored, so the probability 0 it gets multiplies a zero.
+  // tile * 2 + la / 8, rows 2 (la % 8) and 2 (la % 8) + 1 of it), 8-wide dim chunk lb. A tile's
+  // table entry is read one tile before its keys and values, so the keys never wait on a table
+  // read; every load is issued unconditionally (a dead key's address masked to the cache's first
+  // row). Dead keys (past kend, only in the last tile) are masked out of the scores by the causal
+  // mask; their values are zeroed where they are stored, so the probability 0 they get multiplies
+  // a zero.
   const int la = tg & 15, lb = tg >> 4;
+  const int64_t thread_off = (int64_t)(2 * (la % 8)) * tok_stride + (int64_t)kvh * kHeadDim + 8 * lb;
   uint4 kr[2], vr[2];  // [key rr]
-  uint32_t vmask[2];   // all ones for a live key, 0 for a dead one
+  int dead_from = 2;   // keys rr >= dead_from of this thread's pair are dead
   auto tile_of = [&](int i) { return kg + kKeyGroups * i; };  // the group's i-th tile
   auto table_entry = [&](int tile) {
     return btr[min(tile * (kKeyTile / kBlock) + la / 8, a.max_blocks - 1)];
   };
   auto load_tile = [&](int tile, int phys) {
     phys = ((uint32_t)phys < (uint64_t)a.num_blocks) ? phys : 0;
+    const int key = tile * kKeyTile + 2 * la;
+    const bool blk_ok = tile * (kKeyTile / kBlock) + la / 8 < a.max_blocks;
+    const int64_t base = (int64_t)phys * kBlock * tok_stride + thread_off;
+    const int64_t off0 = (blk_ok && key < kend) ? base : 0;
+    const int64_t off1 = (blk_ok && key + 1 < kend) ? base + tok_stride : 0;
+    dead_from = !blk_ok || key >= kend ? 0 : (key + 1 >= kend ? 1 : 2);
+    // loaded as vector values, not struct copies (which the compiler keeps in scratch)
+    const u32x4 k0 = *(const u32x4*)(a.kc + off0);
+    const u32x4 v0 = *(const u32x4*)(a.vc + off0);
+    const u32x4 k1 = *(const u32x4*)(a.kc + off1);
+    const u32x4 v1 = *(const u32x4*)(a.vc + off1);
+    kr[0] = uint4{k0.x, k0.y, k0.z, k0.w};
+    vr[0] = uint4{v0.x, v0.y, v0.z, v0.w};
+    kr[1] = uint4{k1.x, k1.y, k1.z, k1.w};
+    vr[1] = uint4{v1.x, v1.y, v1.z, v1.w};
+  };
+  auto store_tile = [&](int buf, bool last) {
+    uint16_t* K = Ks + buf * kKsTile;
+    uint16_t* V = Vs + buf * kVsTile;
+    if (last) {  // wave-uniform: only the sequence's last tile holds dead keys
+#pragma unroll
+      for (int rr = 0; rr < 2; ++rr)
+        if (rr >= dead_from) vr[rr] = uint4{0u, 0u, 0u, 0u};
+    }
 #pragma unroll
     for (int rr = 0; rr < 2; ++rr) {
-      const int key = tile * kKeyTile + 2 * la + rr;
-      const bool ok = key < kend && key / kBlock < a.max_blocks;
-      const int64_t mask = -(int64_t)ok;
-      const int64_t off =
-          (((int64_t)phys * kBlock + key % kBlock) * tok_stride + (int64_t)kvh * kHeadDim + 8 * lb) & mask;
-      // loaded as vector values, not struct copies (which the compiler keeps in scratch)
-      const u32x4 k = *(const u32x4*)(a.kc + off);
-      const u32x4 v = *(const u32x4*)(a.vc + off);
-      kr[rr] = uint4{k.x, k.y, k.z, k.w};
-      vr[rr] = uint4{v.x, v.y, v.z, v.w};
-      vmask[rr] = (uint32_t)mask;  // applied where the values are stored, not while they load
+      *(uint4*)&K[(2 * la + rr) * kKsStride + 8 * lb] = kr[rr];
+      *(uint4*)&V[(2 * la + rr) * kVsStride + 8 * lb] = vr[rr];
     }
   };
-  auto store_tile = [&](int buf) {
-    uint16_t* K = Ks + buf * kKsTile;
-    uint16_t* V = Vt + buf * kVtTile;
-    const uint32_t live = (vmask[1] & 0xffff0000u) | (vmask[0] & 0x0000ffffu);
-    const uint32_t sel_lo = (0x05040100u & live) | (0x0c0c0c0cu & ~live);
-    const uint32_t sel_hi = (0x07060302u & live) | (0x0c0c0c0cu & ~live);
-#pragma unroll
-    for (int rr = 0; rr < 2; ++rr) *(uint4*)&K[(2 * la + rr) * kKsStride + 8 * lb] = kr[rr];
-    // V^T word of dim 8lb + 2i (+ 1): the low (high) halves of dword i of keys 2la and 2la + 1, one
-    // byte permute each; selector bytes 0x0c give zero bytes for a dead key.
-    const uint32_t v0[4] = {vr[0].x, vr[0].y, vr[0].z, vr[0].w};
-    const uint32_t v1[4] = {vr[1].x, vr[1].y, vr[1].z, vr[1].w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      uint32_t* row = (uint32_t*)&V[(8 * lb + 2 * i) * kVtStride + 2 * la];
-      row[0] = __builtin_amdgcn_perm(v1[i], v0[i], sel_lo);
-      row[kVtStride / 2] = __builtin_amdgcn_perm(v1[i], v0[i], sel_hi);
-    }
-  };
+  auto is_last = [&](int tile) { return (tile + 1) * kKeyTile > kend; };
+  // The PV product's A operand (V^T fragments) straight from the key-major V tile with gfx950's
+  // transposing LDS read: in each 16-lane group, lane i names 4 dims of one key row (row i / 4 of
+  // the group's 4, dims 4 (i % 4)..+3) and lane 4a + c receives dim c of rows a, a + 4, a + 8,
+  // a + 12 -- so lane (grp, j) gets dim dt * 16 + j of keys 4grp..4grp + 3 (and, from the second
+  // read, 16 + 4grp..), the key order of its probabilities.
+  const int vt_off = (4 * grp + (j >> 2)) * kVsStride + 4 * (j & 3);  // element offset, half 0, dt 0
 
   f32x4 acc[8];
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m = -INFINITY, l = 0.f;
+  // Row sums of the probabilities on MFMA: ones (16 x 32) times P gives every lane its query's sum
+  // over the tile's keys, accumulated like the outputs (and rescaled with them).
+  f32x4 lsum = f32x4{0.f, 0.f, 0.f, 0.f};
+  bf16x8 ones;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ones[e] = (__bf16)1.0f;
+  float m = -INFINITY;
 
   // Pipeline per key group: its tile i is computed from LDS buffer i % 2 while the registers
   // receive its tile i + 1; those are written to the other buffer after the MFMAs, then tile i + 2
   // is requested. Both groups run niter iterations, so every barrier is reached by all wavefronts.
   load_tile(tile_of(0), table_entry(tile_of(0)));
   const int ph1 = table_entry(tile_of(1));
-  store_tile(0);
+  store_tile(0, is_last(tile_of(0)));
   if (niter > 1) load_tile(tile_of(1), ph1);
   int ph_next = table_entry(tile_of(2));  // the entry of the group's tile i + 2 at the top of iteration i
   __syncthreads();
@@ -589,7 +606,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
     const int key0 = tile_of(i) * kKeyTile;
     if (key0 <= wave_last) {  // else every query of this wavefront precedes the tile (or it is past kend)
       const uint16_t* K = Ks + buf * kKsTile;
-      const uint16_t* V = Vt + buf * kVtTile;
+      const uint16_t* V = Vs + buf * kVsTile;
       f32x4 sT[2];
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
@@ -600,62 +617,56 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
           sT[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qfrag[ks], sT[mt], 0, 0, 0);
         }
       }
-      // this lane's 8 keys: mt * 16 + 4grp + rr (s8[mt * 4 + rr])
+      // this lane's 8 raw scores q.k: keys mt * 16 + 4grp + rr (s8[mt * 4 + rr])
       float s8[8];
-      if (key0 + kKeyTile - 1 <= wave_first) {  // wave-uniform: the tile is below the diagonal
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) s8[mt * 4 + rr] = sT[mt][rr];
+      if (key0 + kKeyTile - 1 > wave_first) {  // wave-uniform: a tile on the diagonal
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-          for (int rr = 0; rr < 4; ++rr) s8[mt * 4 + rr] = sT[mt][rr] * a.scale_log2;
-      } else {
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-          for (int rr = 0; rr < 4; ++rr) {
-            const int key = key0 + mt * 16 + 4 * grp + rr;
-            s8[mt * 4 + rr] = key <= qpos ? sT[mt][rr] * a.scale_log2 : -INFINITY;
-          }
+          for (int rr = 0; rr < 4; ++rr)
+            if (key0 + mt * 16 + 4 * grp + rr > qpos) s8[mt * 4 + rr] = -INFINITY;
       }
-      float bm = s8[0];
-#pragma unroll
-      for (int e = 1; e < 8; ++e) bm = fmaxf(bm, s8[e]);
-      bm = xrow_max(bm);
+      float bm = fmaxf(fmaxf(fmaxf(s8[0], s8[1]), fmaxf(s8[2], s8[3])), fmaxf(fmaxf(s8[4], s8[5]), fmaxf(s8[6], s8[7])));
+      bm = xrow_max(bm) * a.scale_log2;  // the scale is positive: the maximum of the scaled scores
       // group 0 sees key 0 first, so its maximum is finite from the first tile on; a group-1
       // wavefront whose first visible tile masks a whole row keeps -inf there and adds zeros
       const float mn = fmaxf(m, bm);
       // Rescale only when some row's maximum grew: elsewhere the factor is exp2(0) = 1 exactly.
       if (__builtin_amdgcn_ballot_w64(mn > m)) {
         const float alpha = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m - mn);  // 0 from m = -inf
-        l *= alpha;
+        lsum *= alpha;
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
       }
       m = mn;
+      // p = exp2(s * scale - mn) with one rounding (fma); a row still at -inf subtracts 0 and
+      // gets exp2(-inf) = 0. The hardware exp2: arguments are <= 0 and results below 2^-126 are
+      // negligible against the row's largest weight, 1.
+      const float mb = mn == -INFINITY ? 0.0f : mn;
       bf16x8 pb;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        // the hardware exp2: arguments are <= 0 and results below 2^-126 are negligible against
-        // the row's largest weight, 1; a row still at -inf gets 0
-        const float p = mn == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s8[e] - mn);
-        l += p;
-        pb[e] = (__bf16)p;
-      }
+      for (int e = 0; e < 8; ++e) pb[e] = (__bf16)__builtin_amdgcn_exp2f(__builtin_fmaf(s8[e], a.scale_log2, -mb));
+      lsum = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb, lsum, 0, 0, 0);
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
-        const uint16_t* vrow = V + (dt * 16 + j) * kVtStride + 4 * grp;
-        const uint2 v0 = *(const uint2*)vrow;
-        const uint2 v1 = *(const uint2*)(vrow + 16);
-        const bf16x8 va = __builtin_bit_cast(bf16x8, uint4{v0.x, v0.y, v1.x, v1.y});
+        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(V + vt_off + dt * 16));
+        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(V + vt_off + 16 * kVsStride + dt * 16));
+        const bf16x8 va = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
         acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb, acc[dt], 0, 0, 0);
       }
     }
     if (i + 1 < niter) {
-      store_tile(buf ^ 1);  // buffer of the group's tile i - 1: every wavefront passed the barrier after it
+      store_tile(buf ^ 1, is_last(tile_of(i + 1)));  // buffer of the group's tile i - 1: every wavefront passed the barrier after it
       if (i + 2 < niter) load_tile(tile_of(i + 2), ph_next);
       ph_next = table_entry(tile_of(i + 3));
     }
     __syncthreads();
   }
+  float l = lsum[0];  // the query's sum over every key this group saw (the same in all four)
 
   // Merge: group 1 leaves its state in LDS (over the tile buffers, free after the last barrier);
   // group 0 combines it with its own, lane by lane (the two groups' lanes hold the same rows and
@@ -675,7 +686,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
   const float mm = fmaxf(m, m1);  // finite: group 0 saw key 0
   const float f0 = __builtin_amdgcn_exp2f(m - mm);
   const float f1 = m1 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m1 - mm);
-  l = xrow_sum(l * f0 + l1 * f1);
+  l = l * f0 + l1 * f1;
   if (!qvalid) return;
   const float inv = 1.0f / l;
   uint16_t* orow = a.out + (int64_t)(flat + qi) * a.ldo + (int64_t)head * kHeadDim;
@@ -689,7 +700,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
   }
 }
 
-// The two K / V^T buffers exceed the 64 KB static LDS limit: dynamic LDS, attribute set once.
+// The two groups' K / V buffers exceed the 64 KB static LDS limit: dynamic LDS, attribute set once.
 template <int G>
 static int launch_prefill(const PrefillArgs& a, dim3 grid, hipStream_t s) {
   static bool attr_set = false;
