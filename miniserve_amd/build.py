@@ -21,7 +21,7 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libminiserve_amd.so"
-SOURCES = ["errors.hip", "quant.hip", "gemm_skinny.hip", "gemm_int8.hip", "gemv_rows.hip", "gemv_dec.hip", "gemv_stream.hip", "norm_rope.hip", "attention.hip", "sampler.hip"]
+SOURCES = ["errors.hip", "quant.hip", "gemm_skinny.hip", "gemm_int8.hip", "gemm_big.hip", "gemv_rows.hip", "gemv_dec.hip", "gemv_stream.hip", "norm_rope.hip", "attention.hip", "sampler.hip"]
 ARCH = os.environ.get("MSA_OFFLOAD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [

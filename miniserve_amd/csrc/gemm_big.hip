@@ -1,0 +1,264 @@
+// Int8 weight-only linear for large prefill GEMMs: 256 x 256 output tiles, a wavefront per
+// 128 x 128 quarter.
+//
+// y[m, n] = sum_k x[m, k] * bf16(q[n, k] * s[n]) with float32 accumulation, as Int8Linear.forward
+// (quant/int8.py:35-37) computes it -- the same operands and rounding points as the 128 x 128 GEMM
+// (gemm_int8.hip); only the tiling differs.
+//
+// Why a second tiling: with 64 x 64 wavefront tiles every 16 x 16 x 32 MFMA reads 512 bytes of
+// operand fragments from LDS, about what the CU's LDS delivers per MFMA when all four SIMDs issue
+// them back to back. A 128 x 128 wavefront tile of 32 x 32 x 16 MFMAs reads 8 fragments (8 KB)
+// per 16 MFMAs of twice the work -- half the LDS bytes per flop -- at the price of 256
+// accumulators per lane, which live in the accumulation registers (this file is built without
+// the VGPR-form option of gemm_int8.hip), and of one workgroup per CU.
+//
+//  * Workgroup = 4 wavefronts (2 x 2), 256 tokens x 256 weight rows; per 64-wide K step the
+//    workgroup stages the x tile (256 x 64 bf16, 32 KB) and the dequantized q tile (256 x 64 ->
+//    bf16, 32 KB) in LDS, double buffered (147 KB), the next step's global loads in registers
+//    during the MFMAs, the staging into LDS split into four parts placed after the step's four
+//    16-wide K slices.
+//  * Epilogues: bf16 store; residual add (in place allowed); silu(gate) * up with each
+//    wavefront's 128 weight rows laid out as 64 gate rows then their 64 up rows. Results go
+//    through LDS so that each lane writes 16 contiguous bytes.
+#include <hip/hip_runtime.h>
+
+#include "common.h"
+
+namespace msa {
+
+constexpr int kBM = 256, kBN = 256, kBK = 64;
+constexpr int kBLd = kBK + 8;  // bf16 elements per LDS row (16 bytes of padding)
+constexpr size_t kBigLds = 2 * (size_t)(kBM + kBN) * kBLd * 2;
+
+struct BigGemmArgs {
+  const uint16_t* x;
+  int64_t ldx;
+  const int8_t* w;
+  const uint16_t* scale;
+  uint16_t* y;
+  int64_t ldy;
+  const uint16_t* resid;
+  int64_t ldr;
+  int m, n, k;
+  int n_blocks;  // weight-row blocks (256 rows, or 128 gate + 128 up for SILU_MUL)
+  int m_blocks;  // token blocks of 256
+};
+
+// Weight row held in LDS row r (0..255) of row block nb.
+template <int EPI>
+__device__ __forceinline__ int big_wrow(const BigGemmArgs& a, int nb, int r) {
+  if constexpr (EPI == MSA_EPI_SILU_MUL) {
+    // quarters of 64 rows: gate, up, gate, up -- wavefront column wn owns quarters 2wn, 2wn + 1,
+    // so its accumulator tiles nt and nt + 2 hold the gate and up rows of the same outputs
+    const int q = r >> 6, i = r & 63;
+    return ((q & 1) ? a.n / 2 : 0) + nb * 128 + (q >> 1) * 64 + i;
+  } else {
+    return nb * kBN + r;
+  }
+}
+
+template <int EPI>
+__global__ __launch_bounds__(256) void int8_gemm256_kernel(BigGemmArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t bsm[];
+  uint16_t* As = bsm;                   // [2][256][kBLd]
+  uint16_t* Bs = bsm + 2 * kBM * kBLd;  // [2][256][kBLd]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  const int wm = wave >> 1, wn = wave & 1;
+  // XCD-aware order: the token blocks of one weight block run on one XCD (round-robin dispatch),
+  // so its weight tiles come from HBM once and from that XCD's L2 after.
+  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+  const int nb = (slot / a.m_blocks) * 8 + xcd, mb = slot % a.m_blocks;
+  if (nb >= a.n_blocks) return;  // surplus workgroups of the XCD-rounded grid (whole workgroup)
+  const int m0 = mb * kBM;
+
+  // Loader roles. A: rows tid / 8 + 32 i (i < 8), 8-element chunk tid % 8. B: rows tid / 4 + 64 i
+  // (i < 4), 16-byte chunk tid % 4.
+  const int ar = tid >> 3, ac = (tid & 7) * 8;
+  const int br = tid >> 2, bc = (tid & 3) * 16;
+  // 32-bit byte offsets from the uniform base pointers (the caller checks that they fit), so each
+  // global load takes a scalar base plus one vector register.
+  uint32_t aoff[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int row = min(m0 + ar + 32 * i, a.m - 1);  // rows past m repeat row m - 1; outputs dropped
+    aoff[i] = (uint32_t)(row * (uint32_t)a.ldx + ac) * 2u;
+  }
+  uint32_t boff[4];
+  float bs[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    int row = big_wrow<EPI>(a, nb, br + 64 * i);
+    row = row < a.n ? row : a.n - 1;
+    boff[i] = (uint32_t)row * (uint32_t)a.k + bc;
+    bs[i] = bf16_to_f32(a.scale[row]);
+  }
+  u32x4 ra[8], rb[4];  // native vectors: a struct-typed array stays in private memory
+  auto load_step = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ra[i] = *(const u32x4*)((const char*)a.x + aoff[i] + 2u * k0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) rb[i] = *(const u32x4*)((const char*)a.w + boff[i] + k0);
+  };
+  // Part p of the staged step into LDS buffer buf: p = 0, 1 the x rows 4p..4p+3 (of 8); p = 2, 3 the
+  // weight rows 2(p-2), 2(p-2)+1 (of 4), dequantized.
+  auto store_part = [&](int buf, int p) {
+    if (p < 2) {
+      uint16_t* A_ = As + buf * kBM * kBLd + ar * kBLd + ac;
+#pragma unroll
+      for (int i = 4 * p; i < 4 * p + 4; ++i) *(u32x4*)(A_ + 32 * i * kBLd) = ra[i];
+    } else {
+      uint16_t* B_ = Bs + buf * kBN * kBLd + br * kBLd + bc;
+#pragma unroll
+      for (int i = 2 * (p - 2); i < 2 * (p - 2) + 2; ++i) {
+        // An empty asm redefines rb[i] here, so the compiler cannot start dequantizing the next
+        // step's bytes before the barrier that ends the current one (a wait on loads just issued).
+        asm volatile("" : "+v"(rb[i]));
+        *(bf16x8*)(B_ + 64 * i * kBLd) = dequant8(rb[i].x, rb[i].y, bs[i]);
+        *(bf16x8*)(B_ + 64 * i * kBLd + 8) = dequant8(rb[i].z, rb[i].w, bs[i]);
+      }
+    }
+  };
+
+  // 32 x 32 x 16 MFMAs: 16 accumulator tiles of 16 values. (With 64 tiles of 16 x 16 the register
+  // allocator rotates accumulators through spare registers, two copies per value per K step.)
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = f32x16{};
+
+  const int nk = a.k / kBK;
+  // Loads and stores are unconditional (the last steps reload step nk - 1 and stage it into the
+  // idle buffer: in bounds, never read) so the prefetch registers stay registers and the staging
+  // interleaves with the MFMAs.
+  load_step(0);
+#pragma unroll
+  for (int p = 0; p < 4; ++p) store_part(0, p);
+  load_step(min(1, nk - 1) * kBK);
+  __syncthreads();
+  // MFMA operand fragments: lane (h, r) holds row r of a 32-row tile, K elements 8h..8h+7 of the
+  // 16-wide step.
+  const int r32 = lane & 31, h = lane >> 5;
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    const uint16_t* A = As + cur * kBM * kBLd + (wm * 128 + r32) * kBLd + h * 8;
+    const uint16_t* B = Bs + cur * kBN * kBLd + (wn * 128 + r32) * kBLd + h * 8;
+#pragma unroll
+    for (int ks = 0; ks < kBK / 16; ++ks) {
+      bf16x8 af[4], bfr[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        af[t] = *(const bf16x8*)(A + t * 32 * kBLd + ks * 16);
+        bfr[t] = *(const bf16x8*)(B + t * 32 * kBLd + ks * 16);
+      }
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt)
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mt], bfr[nt], acc[mt][nt], 0, 0, 0);
+      store_part(cur ^ 1, ks);  // step kt + 1 (loaded during step kt - 1 or before the loop)
+    }
+    load_step(min(kt + 2, nk - 1) * kBK);
+    __syncthreads();
+  }
+
+  // Epilogue through LDS (free after the loop's last barrier): each wavefront writes its 128 x 128
+  // quarter (128 x 64 outputs for silu * up) as bf16 into a region of its own, then stores rows
+  // of it with 16-byte writes. Value i of lane (h, r) in tile (mt, nt) is token row
+  // mt*32 + 8(i/4) + 4h + i%4 and weight row nt*32 + r of the quarter.
+  constexpr int kCLd = 128 + 8;  // bf16 elements per staged row
+  uint16_t* Cs = bsm + wave * 128 * kCLd;
+  constexpr int kOutCols = EPI == MSA_EPI_SILU_MUL ? 64 : 128;
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      uint16_t* c = Cs + (mt * 32 + 8 * (i >> 2) + 4 * h + (i & 3)) * kCLd + r32;
+      if constexpr (EPI == MSA_EPI_SILU_MUL) {
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+          const float gt = round_bf16(acc[mt][nt][i]), up = round_bf16(acc[mt][nt + 2][i]);
+          c[nt * 32] = f32_to_bf16(round_bf16(silu_f32(gt)) * up);
+        }
+      } else {
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) c[nt * 32] = f32_to_bf16(acc[mt][nt][i]);
+      }
+    }
+  __syncthreads();  // only wave-local data, but the wavefront's LDS writes must land before its reads
+
+  const int tok0 = m0 + wm * 128;
+  const int col0 = EPI == MSA_EPI_SILU_MUL ? nb * 128 + wn * 64 : nb * kBN + wn * 128;
+  const int out_n = EPI == MSA_EPI_SILU_MUL ? a.n / 2 : a.n;
+  const bool vec = ((uintptr_t)a.y & 15) == 0 && (a.ldy & 7) == 0 &&
+                   (EPI != MSA_EPI_RESIDUAL || (((uintptr_t)a.resid & 15) == 0 && (a.ldr & 7) == 0));
+  constexpr int kChunksPerRow = kOutCols / 8;
+#pragma unroll 4
+  for (int c = lane; c < 128 * kChunksPerRow; c += 64) {
+    const int row = c / kChunksPerRow, cc = (c % kChunksPerRow) * 8;
+    const int tok = tok0 + row, col = col0 + cc;
+    if (tok >= a.m || col >= out_n) continue;
+    const u32x4 v = *(const u32x4*)(Cs + row * kCLd + cc);
+    uint16_t* dst = a.y + (int64_t)tok * a.ldy + col;
+    if (vec && col + 8 <= out_n) {
+      if constexpr (EPI == MSA_EPI_RESIDUAL) {
+        const u32x4 rv = *(const u32x4*)(a.resid + (int64_t)tok * a.ldr + col);
+        u32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          o[e] = pack_bf16x2(bf16lo(v[e]) + bf16lo(rv[e]), bf16hi(v[e]) + bf16hi(rv[e]));
+        *(u32x4*)dst = o;
+      } else {
+        *(u32x4*)dst = v;
+      }
+    } else {  // ragged last columns or unaligned output: element by element
+      const uint16_t* sv = Cs + row * kCLd + cc;
+      for (int e = 0; e < 8 && col + e < out_n; ++e) {
+        float o = bf16_to_f32(sv[e]);
+        if constexpr (EPI == MSA_EPI_RESIDUAL) o += bf16_to_f32(a.resid[(int64_t)tok * a.ldr + col + e]);
+        dst[e] = f32_to_bf16(o);
+      }
+    }
+  }
+}
+
+template <int EPI>
+static int launch_big(const BigGemmArgs& a, int blocks, hipStream_t s) {
+  static bool attr_set = false;  // the dynamic-LDS limit is a per-kernel attribute, set once
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void*)int8_gemm256_kernel<EPI>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kBigLds);
+    if (e != hipSuccess) return fail(MSA_ERR_LAUNCH, std::string("hipFuncSetAttribute: ") + hipGetErrorString(e));
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(int8_gemm256_kernel<EPI>, dim3(blocks), dim3(256), kBigLds, s, a);
+  return check_launch("msa_int8_gemm (256 x 256 tiles)");
+}
+
+// Output tiles of the 256 x 256 tiling (0 when it does not apply: K not a multiple of 64).
+int64_t gemm256_tiles(int64_t m, int64_t n, int64_t k, int epilogue) {
+  if (k % kBK != 0 || (epilogue == MSA_EPI_SILU_MUL && n % 2 != 0)) return 0;
+  const int64_t nbk = epilogue == MSA_EPI_SILU_MUL ? (n / 2 + 127) / 128 : (n + kBN - 1) / kBN;
+  return nbk * ((m + kBM - 1) / kBM);
+}
+
+// The GEMM on 256 x 256 tiles; arguments checked by the caller.
+int gemm256_run(const uint16_t* x, int64_t m, int64_t k, int64_t ldx, const int8_t* qweight, const uint16_t* scale,
+                int64_t n, uint16_t* y, int64_t ldy, int epilogue, const uint16_t* residual, int64_t ldr,
+                hipStream_t s) {
+  BigGemmArgs a{};
+  a.x = x; a.ldx = ldx; a.w = qweight; a.scale = scale; a.y = y; a.ldy = ldy; a.resid = residual; a.ldr = ldr;
+  a.m = (int)m; a.n = (int)n; a.k = (int)k;
+  a.n_blocks = (int)(epilogue == MSA_EPI_SILU_MUL ? (n / 2 + 127) / 128 : (n + kBN - 1) / kBN);
+  a.m_blocks = (int)((m + kBM - 1) / kBM);
+  const int64_t blocks = (int64_t)((a.n_blocks + 7) / 8) * 8 * a.m_blocks;
+  if (blocks > 0x7fffffff) return fail(MSA_ERR_INVALID, "msa_int8_gemm: too many tiles");
+  switch (epilogue) {
+    case MSA_EPI_NONE: return launch_big<MSA_EPI_NONE>(a, (int)blocks, s);
+    case MSA_EPI_SILU_MUL: return launch_big<MSA_EPI_SILU_MUL>(a, (int)blocks, s);
+    default: return launch_big<MSA_EPI_RESIDUAL>(a, (int)blocks, s);
+  }
+}
+
+}  // namespace msa

@@ -57,6 +57,57 @@ def test_gemm_parity(m, n, k):
     assert rel_l2(y.cpu(), exact) < 4e-3
 
 
+# Unsplit GEMMs with 128+ output tiles of 256 x 256 that keep at least as many of the 256 CUs'
+# workgroup slots busy as the 128 x 128 tiling take the 256 x 256-tile kernel: full, ragged-M,
+# ragged-N, one- and three-step K, strided x, all three epilogues.
+GEMM256_SHAPES = [
+    (2048, 5120, 1024),  # 160 tiles
+    (1900, 5000, 192),  # ragged M and N, three K steps
+    (2100, 5000, 64),  # one K step, a ninth token block of 52 rows
+    (4096, 4096, 1024),  # 256 tiles: 32 per XCD
+]
+
+
+@pytest.mark.parametrize("m,n,k", GEMM256_SHAPES)
+@pytest.mark.parametrize("ldx_pad", [0, 64])
+def test_gemm256_parity(m, n, k, ldx_pad):
+    q, s = oi.quantize_int8(_bf16((n, k), seed=n + k + 1, std=0.02))
+    x = _bf16((m, k + ldx_pad), seed=m + 9)
+    xd, qd, sd = x.to(DEV), q.to(DEV), s.to(DEV)
+    assert _native.query("msa_int8_linear_workspace_size", m, n, k) == 0  # never split
+    y = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+    args = (kernels._ptr(xd), m, k, k + ldx_pad, kernels._ptr(qd), kernels._ptr(sd), n)
+    _native.call("msa_int8_gemm", *args, kernels._ptr(y), n, 0, None, 0, kernels._stream(y))
+    y2 = torch.empty_like(y)
+    _native.call("msa_int8_gemm", *args, kernels._ptr(y2), n, 0, None, 0, kernels._stream(y2))
+    assert torch.equal(y, y2)  # deterministic
+    xv = x[:, :k]
+    ref = oi.int8_linear(xv, q, s)
+    exact = xv.double() @ oi.dequantize(q, s, torch.bfloat16).double().T
+    assert rel_l2(y.cpu(), ref) < 1e-2
+    assert rel_l2(y.cpu(), exact) < 4e-3
+    if ldx_pad == 0:  # the model's route: same kernel
+        assert torch.equal(y, kernels.int8_linear(xd, qd, sd))
+    # residual epilogue in place: exact add on the kernel's own product
+    r = _bf16((m, n), seed=m + 10)
+    rd = r.to(DEV)
+    _native.call("msa_int8_gemm", *args, kernels._ptr(rd), n, 2, kernels._ptr(rd), n, kernels._stream(rd))
+    assert torch.equal(rd.cpu(), r + y.cpu())
+
+
+@pytest.mark.parametrize("m,half,k", [(2048, 3072, 1024), (2000, 2600, 128), (2304, 2560, 64)])
+def test_gemm256_silu_mul(m, half, k):
+    n = 2 * half
+    q, s = oi.quantize_int8(_bf16((n, k), seed=m + half, std=0.02))
+    x = _bf16((m, k), seed=m + 4)
+    y = kernels.int8_linear(x.to(DEV), q.to(DEV), s.to(DEV), epilogue=kernels.EPI_SILU_MUL)
+    assert y.shape == (m, half)
+    gate, up = oi.int8_linear(x, q, s).chunk(2, dim=-1)
+    assert rel_l2(y.cpu(), torch.nn.functional.silu(gate) * up) < 1e-2
+    g64, u64 = (x.double() @ oi.dequantize(q, s, torch.bfloat16).double().T).chunk(2, dim=-1)
+    assert rel_l2(y.cpu(), torch.nn.functional.silu(g64) * u64) < 8e-3
+
+
 @pytest.mark.parametrize("m", [128, 333, 2048])
 def test_gemm_silu_mul(m):
     n, k = 6144, 1024
