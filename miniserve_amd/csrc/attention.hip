@@ -498,7 +498,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
   uint16_t* Ks = psm + kg * 2 * (kKsTile + kVsTile);  // [2][kKeyTile][kKsStride]
   uint16_t* Vs = Ks + 2 * kKsTile;                     // [2][kKeyTile][kVsStride]
 
-  const int wi = blockIdx.x, kvh = blockIdx.y;
+  // KV head fastest in dispatch order: workgroups go round-robin over the 8 XCDs, so with 8 KV
+  // heads each XCD serves one head and its L2 holds that head's keys and values for every query
+  // tile (work items stay longest first).
+  const int lin = blockIdx.x + gridDim.x * blockIdx.y;
+  const int kvh = lin % a.kv_heads, wi = lin / a.kv_heads;
   const int seq = a.work[2 * wi], tstart = a.work[2 * wi + 1];
   const int flat = a.seq_info[3 * seq], nnew = a.seq_info[3 * seq + 1], ncached = a.seq_info[3 * seq + 2];
   const int lane = threadIdx.x & 63, wave = tg >> 6;  // wavefront within the key group
