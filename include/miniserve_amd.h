@@ -280,6 +280,22 @@ int msa_paged_attention_decode_qkv(const uint16_t* qkv, int64_t ldqkv, const uin
                                    int partition_tokens, int max_partitions, float scale, uint16_t* out,
                                    int64_t ldo, void* workspace, size_t workspace_bytes, msa_stream_t stream);
 
+/* The qkv projection of a prefill-sized batch with the per-head q/k RMSNorm, RoPE and KV-cache
+ * write of msa_qk_norm_rope_cache in its epilogue (model/qwen3.py:94-98, then the cache write of
+ * attention/backends.py:159-160): y = x @ bf16(q * s)^T as msa_int8_gemm computes it
+ * (float32 sums rounded to bf16, never split over K), n = (heads + 2 kv_heads) * 128 weight rows
+ * whose 128-row blocks are the head slots (q heads, k heads, v heads); then the same rounding
+ * steps as msa_qk_norm_rope_cache, bit for bit: q_out [m, heads, 128] gets the normed, rotated
+ * queries, k_cache / v_cache [num_slots, kv_heads, 128] the normed, rotated keys and the values at
+ * slot_mapping[t] (slots outside [0, num_slots) are skipped). cos / sin are [m, 128] float32.
+ * head_dim must be 128; x, the norm weights, cos / sin, q_out and the caches 16-byte aligned. */
+int msa_int8_gemm_qk_norm_rope_cache(const uint16_t* x, int64_t m, int64_t k, int64_t ldx, const int8_t* qweight,
+                                     const uint16_t* scale, int heads, int kv_heads, int head_dim,
+                                     const uint16_t* q_norm_w, const uint16_t* k_norm_w, float eps,
+                                     const float* cos, const float* sin, const int64_t* slot_mapping,
+                                     uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache, int64_t num_slots,
+                                     msa_stream_t stream);
+
 /* The prefill path of paged_attention (attention/backends.py:182-196) for chunks of any length,
  * fresh or continuing from cached keys: causal attention of each new token over positions
  * 0..its own, keys and values read through the block table from the caches (which already hold

@@ -16,7 +16,7 @@ from pathlib import Path
 import torch  # noqa: F401  -- must be imported before the HIP library is loaded
 
 LIB_PATH = Path(__file__).resolve().parent / "libminiserve_amd.so"
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 # name -> (restype, argtypes); mirrors include/miniserve_amd.h.
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
@@ -123,6 +123,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [c_void_p, c_int64, c_void_p, c_void_p, c_float, c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_void_p,
          c_int64, c_int, c_int, c_int, c_int, c_void_p, c_int, c_void_p, c_void_p, c_int, c_int, c_int, c_float,
          c_void_p, c_int64, c_void_p, c_size_t, c_void_p],
+    ),
+    "msa_int8_gemm_qk_norm_rope_cache": (
+        c_int,
+        [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p, c_void_p, c_float,
+         c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p],
     ),
     "msa_paged_attention_prefill": (
         c_int,

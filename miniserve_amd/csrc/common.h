@@ -41,6 +41,34 @@ __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to
 __device__ __forceinline__ float silu_f32(float x) {
   return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * kLog2e));
 }
+// Per-head RMSNorm then RoPE of one 128-dim head row (model/layers.py:18-22, 56-65 rounding: y =
+// bf16(w * bf16(x * r)), out = bf16(y0 * c) + bf16(-y1 * s), bf16(y1 * c) + bf16(y0 * s), each
+// product rounded, the sum rounded by the caller's store) held by eight consecutive lanes: lane
+// sub holds dims [8 sub, 8 sub + 8) in lo and their rotary partners [64 + 8 sub, ...) in hi, the
+// norm weights of those dims in nl / nh and the float32 cos / sin of the position in cl, ch, sl,
+// sh. The sum of squares adds each lane's 16 squares in order, then meets over the eight lanes.
+__device__ __forceinline__ void head_norm_rope8(const float (&lo)[8], const float (&hi)[8], const uint4& nl,
+                                                const uint4& nh, const float (&cl)[8], const float (&ch)[8],
+                                                const float (&sl)[8], const float (&sh)[8], float eps, float (&ol)[8],
+                                                float (&oh)[8]) {
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss += lo[e] * lo[e] + hi[e] * hi[e];
+  ss += __shfl_xor(ss, 1);
+  ss += __shfl_xor(ss, 2);
+  ss += __shfl_xor(ss, 4);
+  const float r = 1.0f / sqrtf(ss / 128.0f + eps);
+  const uint32_t wl[4] = {nl.x, nl.y, nl.z, nl.w}, wh[4] = {nh.x, nh.y, nh.z, nh.w};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float wlo = (e & 1) ? bf16hi(wl[e >> 1]) : bf16lo(wl[e >> 1]);
+    const float whi = (e & 1) ? bf16hi(wh[e >> 1]) : bf16lo(wh[e >> 1]);
+    const float a = round_bf16(wlo * round_bf16(lo[e] * r));
+    const float b = round_bf16(whi * round_bf16(hi[e] * r));
+    ol[e] = round_bf16(a * round_bf16(cl[e])) + round_bf16(-b * round_bf16(sl[e]));
+    oh[e] = round_bf16(b * round_bf16(ch[e])) + round_bf16(a * round_bf16(sh[e]));
+  }
+}
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x8_t __attribute__((ext_vector_type(8)));
 // Two floats -> a bf16 pair (round to nearest even) in one v_cvt_pk_bf16_f32; converting the

@@ -22,4 +22,4 @@ int check_launch(const char* what) {
 
 extern "C" const char* msa_last_error(void) { return msa::g_last_error.c_str(); }
 
-extern "C" int msa_abi_version(void) { return 14; }
+extern "C" int msa_abi_version(void) { return 15; }

@@ -37,9 +37,23 @@ struct GemmArgs {
   int m_blocks;  // token blocks of 128
   int k_per;     // K per split (a multiple of 64; == k without split-K)
   float* part;   // split-K: float32 partials [splits][m][n]
+  // kEpiQkNorm: the qkv projection's epilogue -- per-head RMSNorm + RoPE of q and k, q rows out,
+  // k and v into the paged caches at slots[token] (weight block nb is head slot nb)
+  int heads, kv_heads;
+  const uint16_t* qw;
+  const uint16_t* kw;
+  float eps;
+  const float* cos_t;
+  const float* sin_t;
+  const int64_t* slots;
+  uint16_t* q_out;
+  uint16_t* k_cache;
+  uint16_t* v_cache;
+  int64_t num_slots;
 };
 
 constexpr int kEpiPartial = 3;  // split-K: store the float32 accumulators, no rounding
+constexpr int kEpiQkNorm = 4;   // qkv + q/k RMSNorm + RoPE + KV cache write (head_dim 128)
 
 
 // Weight row held in LDS row r (0..127) of row block nb.
@@ -161,38 +175,130 @@ __global__ __launch_bounds__(256) void int8_gemm_kernel(GemmArgs a) {
 #undef MSA_GEMM_COMPUTE
 
   // lane (g, j) of tile (mt, nt): tokens m0 + wm*64 + mt*16 + 4g + i, LDS weight row wn*64 + nt*16 + j
+  if constexpr (EPI == kEpiPartial) {
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
+    for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int tok = m0 + wm * 64 + mt * 16 + 4 * g + i;
-      if (tok >= a.m) continue;
-      if constexpr (EPI == kEpiPartial) {
+      for (int i = 0; i < 4; ++i) {
+        const int tok = m0 + wm * 64 + mt * 16 + 4 * g + i;
+        if (tok >= a.m) continue;
         float* prow = a.part + ((int64_t)ks * a.m + tok) * a.n;
 #pragma unroll
         for (int nt = 0; nt < 4; ++nt) {
           const int col = nb * kGBN + wn * 64 + nt * 16 + j;
           if (col < a.n) prow[col] = acc[mt][nt][i];
         }
-      } else if constexpr (EPI == MSA_EPI_SILU_MUL) {
+      }
+  } else {
+    // The tile's bf16 outputs go through LDS (free once every wavefront is past its last K step):
+    // rows are then stored 16 bytes per lane, or handed to the q/k-norm epilogue whole.
+    constexpr int kCLd = kGBN + 8;
+    uint16_t* Cs = gsm;  // [128 tokens][kCLd]
+    __syncthreads();
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-          const int col = nb * 64 + wn * 32 + nt * 16 + j;
-          if (col >= a.n / 2) continue;
-          const float gt = round_bf16(acc[mt][nt][i]), up = round_bf16(acc[mt][nt + 2][i]);
-          a.y[(int64_t)tok * a.ldy + col] = f32_to_bf16(round_bf16(silu_f32(gt)) * up);
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint16_t* c = Cs + (wm * 64 + mt * 16 + 4 * g + i) * kCLd + j;
+        if constexpr (EPI == MSA_EPI_SILU_MUL) {
+#pragma unroll
+          for (int nt = 0; nt < 2; ++nt) {
+            const float gt = round_bf16(acc[mt][nt][i]), up = round_bf16(acc[mt][nt + 2][i]);
+            c[wn * 32 + nt * 16] = f32_to_bf16(round_bf16(silu_f32(gt)) * up);
+          }
+        } else {
+#pragma unroll
+          for (int nt = 0; nt < 4; ++nt) c[wn * 64 + nt * 16] = f32_to_bf16(acc[mt][nt][i]);
         }
-      } else {
+      }
+    __syncthreads();
+    if constexpr (EPI == kEpiQkNorm) {
+      // Eight threads per token row, as the standalone q/k-norm kernel: thread sub holds dims
+      // [8 sub, 8 sub + 8) and their rotary partners [64 + 8 sub, ...).
+      const int hs = nb, sub = tid & 7;
+      const bool is_q = hs < a.heads, is_v = hs >= a.heads + a.kv_heads;
+      const int d0 = 8 * sub, d1 = 64 + 8 * sub;
+      const uint16_t* nw = is_q ? a.qw : a.kw;
+      const uint4 nl = *(const uint4*)(nw + d0), nh = *(const uint4*)(nw + d1);
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt) {
-          const int col = nb * kGBN + wn * 64 + nt * 16 + j;
-          if (col >= a.n) continue;
-          float v = round_bf16(acc[mt][nt][i]);
-          if constexpr (EPI == MSA_EPI_RESIDUAL) v += bf16_to_f32(a.resid[(int64_t)tok * a.ldr + col]);
-          a.y[(int64_t)tok * a.ldy + col] = f32_to_bf16(v);
+      for (int pass = 0; pass < kGBM / 32; ++pass) {
+        const int row = pass * 32 + (tid >> 3);
+        const int64_t t = m0 + row;
+        if (t >= a.m) continue;  // the same for the eight threads of a row
+        const u32x4 ul = *(const u32x4*)(Cs + row * kCLd + d0), uh = *(const u32x4*)(Cs + row * kCLd + d1);
+        const int64_t slot = a.slots[t];
+        const bool cached = slot >= 0 && slot < a.num_slots;
+        if (is_v) {
+          if (cached) {
+            uint16_t* dst = a.v_cache + (slot * a.kv_heads + (hs - a.heads - a.kv_heads)) * 128;
+            *(u32x4*)(dst + d0) = ul;
+            *(u32x4*)(dst + d1) = uh;
+          }
+          continue;
+        }
+        float lo[8], hi[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          lo[2 * e] = bf16lo(ul[e]);
+          lo[2 * e + 1] = bf16hi(ul[e]);
+          hi[2 * e] = bf16lo(uh[e]);
+          hi[2 * e + 1] = bf16hi(uh[e]);
+        }
+        const float* cr = a.cos_t + t * 128;
+        const float* sr = a.sin_t + t * 128;
+        const float4 cl0 = *(const float4*)(cr + d0), cl1 = *(const float4*)(cr + d0 + 4);
+        const float4 ch0 = *(const float4*)(cr + d1), ch1 = *(const float4*)(cr + d1 + 4);
+        const float4 sl0 = *(const float4*)(sr + d0), sl1 = *(const float4*)(sr + d0 + 4);
+        const float4 sh0 = *(const float4*)(sr + d1), sh1 = *(const float4*)(sr + d1 + 4);
+        const float cl[8] = {cl0.x, cl0.y, cl0.z, cl0.w, cl1.x, cl1.y, cl1.z, cl1.w};
+        const float ch[8] = {ch0.x, ch0.y, ch0.z, ch0.w, ch1.x, ch1.y, ch1.z, ch1.w};
+        const float sl[8] = {sl0.x, sl0.y, sl0.z, sl0.w, sl1.x, sl1.y, sl1.z, sl1.w};
+        const float sh[8] = {sh0.x, sh0.y, sh0.z, sh0.w, sh1.x, sh1.y, sh1.z, sh1.w};
+        float ol[8], oh[8];
+        head_norm_rope8(lo, hi, nl, nh, cl, ch, sl, sh, a.eps, ol, oh);
+        if (!is_q && !cached) continue;
+        uint16_t* dst = is_q ? a.q_out + (t * a.heads + hs) * 128 : a.k_cache + (slot * a.kv_heads + (hs - a.heads)) * 128;
+        *(uint4*)(dst + d0) = uint4{pack_bf16x2(ol[0], ol[1]), pack_bf16x2(ol[2], ol[3]), pack_bf16x2(ol[4], ol[5]),
+                                    pack_bf16x2(ol[6], ol[7])};
+        *(uint4*)(dst + d1) = uint4{pack_bf16x2(oh[0], oh[1]), pack_bf16x2(oh[2], oh[3]), pack_bf16x2(oh[4], oh[5]),
+                                    pack_bf16x2(oh[6], oh[7])};
+      }
+    } else {
+      constexpr int kOutCols = EPI == MSA_EPI_SILU_MUL ? 64 : kGBN;
+      constexpr int kChunksPerRow = kOutCols / 8;
+      const int col0 = EPI == MSA_EPI_SILU_MUL ? nb * 64 : nb * kGBN;
+      const int out_n = EPI == MSA_EPI_SILU_MUL ? a.n / 2 : a.n;
+      const bool vec = ((uintptr_t)a.y & 15) == 0 && (a.ldy & 7) == 0 &&
+                       (EPI != MSA_EPI_RESIDUAL || (((uintptr_t)a.resid & 15) == 0 && (a.ldr & 7) == 0));
+#pragma unroll 4
+      for (int c = tid; c < kGBM * kChunksPerRow; c += 256) {
+        const int row = c / kChunksPerRow, cc = (c % kChunksPerRow) * 8;
+        const int tok = m0 + row, col = col0 + cc;
+        if (tok >= a.m || col >= out_n) continue;
+        const u32x4 v = *(const u32x4*)(Cs + row * kCLd + cc);
+        uint16_t* dst = a.y + (int64_t)tok * a.ldy + col;
+        if (vec && col + 8 <= out_n) {
+          if constexpr (EPI == MSA_EPI_RESIDUAL) {
+            const u32x4 rv = *(const u32x4*)(a.resid + (int64_t)tok * a.ldr + col);
+            u32x4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              o[e] = pack_bf16x2(bf16lo(v[e]) + bf16lo(rv[e]), bf16hi(v[e]) + bf16hi(rv[e]));
+            *(u32x4*)dst = o;
+          } else {
+            *(u32x4*)dst = v;
+          }
+        } else {  // ragged last columns or unaligned output: element by element
+          const uint16_t* sv = Cs + row * kCLd + cc;
+          for (int e = 0; e < 8 && col + e < out_n; ++e) {
+            float o = bf16_to_f32(sv[e]);
+            if constexpr (EPI == MSA_EPI_RESIDUAL) o += bf16_to_f32(a.resid[(int64_t)tok * a.ldr + col + e]);
+            dst[e] = f32_to_bf16(o);
+          }
         }
       }
     }
+  }
 }
 
 template <int EPI>
@@ -569,6 +675,43 @@ int launch_lm_gemm(const uint16_t* hidden, int64_t ld_hidden, int64_t hidden_row
 }  // namespace msa
 
 using namespace msa;
+
+extern "C" int msa_int8_gemm_qk_norm_rope_cache(const uint16_t* x, int64_t m, int64_t k, int64_t ldx,
+                                               const int8_t* qweight, const uint16_t* scale, int heads, int kv_heads,
+                                               int head_dim, const uint16_t* q_norm_w, const uint16_t* k_norm_w,
+                                               float eps, const float* cos, const float* sin,
+                                               const int64_t* slot_mapping, uint16_t* q_out, uint16_t* k_cache,
+                                               uint16_t* v_cache, int64_t num_slots, msa_stream_t stream) {
+  const char* who = "msa_int8_gemm_qk_norm_rope_cache";
+  if (m == 0) return MSA_OK;
+  if (!x || !qweight || !scale || !q_norm_w || !k_norm_w || !cos || !sin || !slot_mapping || !q_out || !k_cache ||
+      !v_cache)
+    return fail(MSA_ERR_INVALID, std::string(who) + ": null pointer");
+  if (head_dim != 128) return fail(MSA_ERR_UNSUPPORTED, std::string(who) + ": head_dim must be 128");
+  if (m < 0 || k <= 0 || m > 0x7fffffff || k > 0x7fffffff || heads <= 0 || kv_heads <= 0 || num_slots < 0)
+    return fail(MSA_ERR_INVALID, std::string(who) + ": bad shape");
+  if (k % kGBK != 0) return fail(MSA_ERR_UNSUPPORTED, std::string(who) + ": in_features must be a multiple of 64");
+  if (ldx < k || ldx % 8 != 0 || !aligned16(x) || !aligned16(qweight))
+    return fail(MSA_ERR_INVALID, std::string(who) + ": x / qweight must be 16-byte aligned with ldx % 8 == 0");
+  if (!aligned16(q_norm_w) || !aligned16(k_norm_w) || !aligned16(cos) || !aligned16(sin) || !aligned16(q_out) ||
+      !aligned16(k_cache) || !aligned16(v_cache))
+    return fail(MSA_ERR_INVALID, std::string(who) + ": norm weights, cos / sin, q_out and caches must be 16-byte aligned");
+  const int64_t n = (int64_t)(heads + 2 * kv_heads) * 128;
+  GemmArgs a{};
+  a.x = x; a.ldx = ldx; a.w = qweight; a.scale = scale;
+  a.m = (int)m; a.n = (int)n; a.k = (int)k;
+  a.n_blocks = heads + 2 * kv_heads;
+  a.m_blocks = (int)((m + kGBM - 1) / kGBM);
+  a.k_per = (int)k;
+  a.heads = heads; a.kv_heads = kv_heads; a.qw = q_norm_w; a.kw = k_norm_w; a.eps = eps;
+  a.cos_t = cos; a.sin_t = sin; a.slots = slot_mapping; a.q_out = q_out; a.k_cache = k_cache; a.v_cache = v_cache;
+  a.num_slots = num_slots;
+  const int64_t blocks = (int64_t)a.n_blocks * a.m_blocks;
+  if (blocks > 0x7fffffff) return fail(MSA_ERR_INVALID, std::string(who) + ": too many tiles");
+  const int rc = launch_gemm<kEpiQkNorm>(a, (int)blocks, (hipStream_t)stream);
+  if (rc != MSA_OK) return rc;
+  return check_launch(who);
+}
 
 extern "C" int msa_int8_gemm(const uint16_t* x, int64_t m, int64_t k, int64_t ldx, const int8_t* qweight,
                              const uint16_t* scale, int64_t n, uint16_t* y, int64_t ldy, int epilogue,

@@ -240,28 +240,12 @@ __global__ __launch_bounds__(256) void qk_norm_rope_cache_d128_kernel(
     }
     return;  // the eight threads of a head slot leave together
   }
-  float ss = 0.f;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) ss += lo[e] * lo[e] + hi[e] * hi[e];
-  ss += __shfl_xor(ss, 1);
-  ss += __shfl_xor(ss, 2);
-  ss += __shfl_xor(ss, 4);
-  const float r = 1.0f / sqrtf(ss / (float)D + eps);
-  const uint32_t wl[4] = {nl.x, nl.y, nl.z, nl.w}, wh[4] = {nh.x, nh.y, nh.z, nh.w};
   const float cl[8] = {cl0.x, cl0.y, cl0.z, cl0.w, cl1.x, cl1.y, cl1.z, cl1.w};
   const float ch[8] = {ch0.x, ch0.y, ch0.z, ch0.w, ch1.x, ch1.y, ch1.z, ch1.w};
   const float sl[8] = {sl0.x, sl0.y, sl0.z, sl0.w, sl1.x, sl1.y, sl1.z, sl1.w};
   const float sh[8] = {sh0.x, sh0.y, sh0.z, sh0.w, sh1.x, sh1.y, sh1.z, sh1.w};
   float ol[8], oh[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float wlo = (e & 1) ? bf16hi(wl[e >> 1]) : bf16lo(wl[e >> 1]);
-    const float whi = (e & 1) ? bf16hi(wh[e >> 1]) : bf16lo(wh[e >> 1]);
-    const float a = round_bf16(wlo * round_bf16(lo[e] * r));
-    const float b = round_bf16(whi * round_bf16(hi[e] * r));
-    ol[e] = round_bf16(a * round_bf16(cl[e])) + round_bf16(-b * round_bf16(sl[e]));
-    oh[e] = round_bf16(b * round_bf16(ch[e])) + round_bf16(a * round_bf16(sh[e]));
-  }
+  head_norm_rope8(lo, hi, nl, nh, cl, ch, sl, sh, eps, ol, oh);
   if (!live || (!is_q && !cached)) return;
   uint16_t* dst = is_q ? q_out + (t * heads + hsc) * D : k_cache + (slot * kv_heads + (hsc - heads)) * D;
   *(uint4*)(dst + d0) = uint4{pack_bf16x2(ol[0], ol[1]), pack_bf16x2(ol[2], ol[3]), pack_bf16x2(ol[4], ol[5]),

@@ -295,6 +295,52 @@ def qk_norm_rope_cache(
     return q
 
 
+def qkv_gemm_fuses_norm(m: int, heads: int, kv_heads: int, head_dim: int, k: int) -> bool:
+    """Whether the qkv projection of ``m`` tokens takes the unsplit prefill GEMM, whose epilogue can
+    apply the q/k-norm, RoPE and cache write (``int8_linear_qk_norm_rope_cache``)."""
+    n = (heads + 2 * kv_heads) * head_dim
+    return (head_dim == 128 and m >= 128 and k % 64 == 0
+            and _native.query("msa_int8_linear_workspace_size", m, n, k) == 0)
+
+
+def int8_linear_qk_norm_rope_cache(
+    x: Tensor,
+    qweight: Tensor,
+    scale: Tensor,
+    heads: int,
+    kv_heads: int,
+    head_dim: int,
+    q_norm_w: Tensor,
+    k_norm_w: Tensor,
+    eps: float,
+    cos: Tensor,
+    sin: Tensor,
+    slot_mapping: Tensor,
+    k_cache: Tensor,
+    v_cache: Tensor,
+) -> Tensor:
+    """``qk_norm_rope_cache(int8_linear(x, qweight, scale), ...)`` in one GEMM whose epilogue norms and
+    rotates q and k and writes k / v to the cache -- the same values bit for bit; returns q [T, H, D]."""
+    _on_gpu(x, qweight, scale, q_norm_w, k_norm_w, cos, sin, slot_mapping, k_cache, v_cache)
+    t, k = x.shape
+    _check(x.dtype == torch.bfloat16 and x.stride(-1) == 1, "int8_linear_qk_norm_rope_cache: x bf16 rows")
+    _check(qweight.dtype == torch.int8 and qweight.is_contiguous()
+           and qweight.shape == ((heads + 2 * kv_heads) * head_dim, k), "int8_linear_qk_norm_rope_cache: qweight")
+    _check(scale.dtype == torch.bfloat16 and scale.numel() == qweight.shape[0], "int8_linear_qk_norm_rope_cache: scale")
+    _check(cos.dtype == torch.float32 and cos.shape == (t, head_dim) and cos.is_contiguous(), "cos [T, D] float32")
+    _check(sin.dtype == torch.float32 and sin.shape == (t, head_dim) and sin.is_contiguous(), "sin [T, D] float32")
+    _check(slot_mapping.dtype == torch.int64 and slot_mapping.numel() == t, "slot_mapping [T] int64")
+    _check(k_cache.is_contiguous() and v_cache.is_contiguous() and k_cache.shape == v_cache.shape, "caches")
+    _check(k_cache.shape[-2:] == (kv_heads, head_dim), "cache layout [slots, KVH, D]")
+    q = torch.empty(t, heads, head_dim, dtype=torch.bfloat16, device=x.device)
+    _native.call(
+        "msa_int8_gemm_qk_norm_rope_cache", _ptr(x), t, k, x.stride(0), _ptr(qweight), _ptr(scale), heads, kv_heads,
+        head_dim, _ptr(q_norm_w), _ptr(k_norm_w), float(eps), _ptr(cos), _ptr(sin), _ptr(slot_mapping), _ptr(q),
+        _ptr(k_cache), _ptr(v_cache), k_cache.shape[0], _stream(x),
+    )
+    return q
+
+
 def reshape_and_cache(k: Tensor, v: Tensor, k_cache: Tensor, v_cache: Tensor, slot_mapping: Tensor) -> None:
     """k_cache[slot_mapping] = k; v_cache[slot_mapping] = v (attention/backends.py:159-160)."""
     _on_gpu(k, v, k_cache, v_cache, slot_mapping)

@@ -311,8 +311,8 @@ class Qwen3ForCausalLM(nn.Module):
     ) -> Tensor:
         """Decoder layer ``i`` (model/qwen3.py:112-122) for prefill-sized batches: int8 linears on the
         LDS-tiled MFMA GEMM (silu * up in its epilogue; the o and down projections add the residual
-        and apply the next RMSNorm, merging split-K partials in the same pass) and q/k-norm + RoPE +
-        KV write as its own kernel. ``x`` is the residual stream (updated in place), ``h`` its
+        and apply the next RMSNorm, merging split-K partials in the same pass; q/k-norm + RoPE +
+        KV write in the qkv GEMM's epilogue when that GEMM is unsplit, else as its own kernel). ``x`` is the residual stream (updated in place), ``h`` its
         input RMSNorm; returns the next layer's normed input (the final norm after the last layer)."""
         cfg = self.cfg
         t = x.shape[0]
@@ -320,10 +320,17 @@ class Qwen3ForCausalLM(nn.Module):
         layer = layers[i]
         attn, mlp = layer.self_attn, layer.mlp
         qkv, o, gu, dn = attn.qkv_proj, attn.o_proj, mlp.gate_up_proj, mlp.down_proj
-        q = kernels.qk_norm_rope_cache(
-            kernels.int8_linear(h, qkv.qweight, qkv.kscale), attn.num_heads, attn.num_kv_heads, attn.head_dim,
-            attn.q_norm.weight, attn.k_norm.weight, attn.q_norm.eps, cos, sin, meta.slot_mapping, k_cache, v_cache,
-        )
+        if kernels.qkv_gemm_fuses_norm(t, attn.num_heads, attn.num_kv_heads, attn.head_dim, h.shape[-1]):
+            q = kernels.int8_linear_qk_norm_rope_cache(
+                h, qkv.qweight, qkv.kscale, attn.num_heads, attn.num_kv_heads, attn.head_dim, attn.q_norm.weight,
+                attn.k_norm.weight, attn.q_norm.eps, cos, sin, meta.slot_mapping, k_cache, v_cache,
+            )
+        else:
+            q = kernels.qk_norm_rope_cache(
+                kernels.int8_linear(h, qkv.qweight, qkv.kscale), attn.num_heads, attn.num_kv_heads, attn.head_dim,
+                attn.q_norm.weight, attn.k_norm.weight, attn.q_norm.eps, cos, sin, meta.slot_mapping, k_cache,
+                v_cache,
+            )
         a = attend(q, k_cache, v_cache, meta, attn.scale).view(t, attn.q_size)
         post = layer.post_attention_layernorm
         hn = kernels.int8_linear_add_rmsnorm(a, o.qweight, o.kscale, x, post.weight, post.eps)

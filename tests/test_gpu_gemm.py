@@ -152,3 +152,41 @@ def test_linear_add_rmsnorm(m, n, k):
     assert rel_l2(h1.cpu(), h2.cpu()) < 2e-3  # sums of squares in another float32 order
     ref = ol.rms_norm(r + oi.int8_linear(x, q, s), w, 1e-6)
     assert rel_l2(h1.cpu(), ref) < 1e-2
+
+
+@pytest.mark.parametrize("m,heads,kv_heads,k", [(2048, 16, 8, 1024), (300, 32, 8, 1024), (129, 8, 8, 2048)])
+def test_gemm_qk_norm_rope_cache_matches_unfused(m, heads, kv_heads, k):
+    """The qkv GEMM with the q/k-norm + RoPE + cache write in its epilogue against the unsplit GEMM
+    followed by the standalone kernel (pinned against the oracle in test_gpu_kernels.py): the same
+    q and caches bit for bit, including skipped slots (-1 and past the pool); and q within the
+    oracle's bar."""
+    d = 128
+    n = (heads + 2 * kv_heads) * d
+    qw8, sc = oi.quantize_int8(_bf16((n, k), seed=m + heads, std=0.02))
+    x = _bf16((m, k), seed=m + 7)
+    gen = torch.Generator().manual_seed(m)
+    nq = (1 + 0.1 * torch.randn(d, generator=gen)).to(torch.bfloat16)
+    nk = (1 + 0.1 * torch.randn(d, generator=gen)).to(torch.bfloat16)
+    cos_t, sin_t = ol.rope_tables(d, 4096, 1e6)
+    pos = torch.randint(0, 4096, (m,), generator=gen)
+    num_slots = m + 64
+    slots = torch.randperm(num_slots, generator=gen)[:m]
+    slots[3] = -1
+    slots[m // 2] = num_slots + 5  # past the pool: skipped
+    xd, qd, sd = x.to(DEV), qw8.to(DEV), sc.to(DEV)
+    args = (nq.to(DEV), nk.to(DEV), 1e-6, cos_t[pos].contiguous().to(DEV), sin_t[pos].contiguous().to(DEV), slots.to(DEV))
+    kc1 = torch.zeros(num_slots, kv_heads, d, dtype=torch.bfloat16, device=DEV)
+    vc1, kc2, vc2 = torch.zeros_like(kc1), torch.zeros_like(kc1), torch.zeros_like(kc1)
+    q1 = kernels.int8_linear_qk_norm_rope_cache(xd, qd, sd, heads, kv_heads, d, *args, kc1, vc1)
+    qkv = torch.empty(m, n, dtype=torch.bfloat16, device=DEV)
+    _native.call("msa_int8_gemm", kernels._ptr(xd), m, k, k, kernels._ptr(qd), kernels._ptr(sd), n, kernels._ptr(qkv),
+                 n, 0, None, 0, kernels._stream(qkv))  # unsplit
+    q2 = kernels.qk_norm_rope_cache(qkv, heads, kv_heads, d, *args, kc2, vc2)
+    assert torch.equal(q1, q2)
+    assert torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
+    assert int(torch.count_nonzero(kc1.abs().sum((1, 2)))) == m - 2  # two rows skipped
+    ref = oi.int8_linear(x, qw8, sc)
+    qn = ol.rms_norm(ref[:, : heads * d].reshape(m, heads, d), nq, 1e-6)
+    kn = ol.rms_norm(ref[:, heads * d : (heads + kv_heads) * d].reshape(m, kv_heads, d), nk, 1e-6)
+    qo, _ = ol.apply_rope(qn, kn, cos_t[pos], sin_t[pos])
+    assert rel_l2(q1.cpu(), qo) < 1e-2
