@@ -560,7 +560,22 @@ def bench_prefill(args) -> dict:
                           "1984-token prompt chunk; eager step (prepare + forward + fused LM head/argmax + sync)",
                           "tokens": tokens, "step_tflop": round(step_flops / 1e12, 3),
                           "step_tflop_s": round(step_flops / dt / 1e12, 1)})
-    out["roofline"] = roofline("int8_gemm_kernel<SILU_MUL> (gate_up, M=2048)", "mfma", flops / secs / 1e12, flops, secs)
+    # the step's largest kernel by time: the chunk's causal attention (the decode rows' attention
+    # runs beside it on a second stream), timed alone over the 28 layers' KV pools
+    from miniserve_amd.attention import backends as hb
+
+    pslots = torch.tensor([dec.num_blocks * 16 + p for p in range(chunk)], device=dev)
+    pmeta = hb.build_attention_metadata([hb.SeqChunk(0, chunk, 0, list(range(dec.num_blocks, total_blocks)))],
+                                        pslots, 16)
+    pq = torch.randn(chunk, 16, 128, device=dev).to(torch.bfloat16)
+    caches = runner.kv_caches
+    asecs = hip_time(lambda i: hb.attend(pq, caches[i][0], caches[i][1], pmeta, 128**-0.5), len(caches))
+    aflops = 4 * 16 * 128 * (chunk * (chunk + 1) // 2)
+    log(f"prefill attention (1984-token causal chunk): {asecs * 1e6:.1f} us, {aflops / asecs / 1e12:.1f} TFLOP/s")
+    out["roofline"] = roofline("paged_prefill_kernel<2> (1984-token causal chunk, 16 q / 8 KV heads)", "mfma",
+                               aflops / asecs / 1e12, aflops, asecs)
+    out["roofline_gemm"] = roofline("int8_gemm256_kernel<1> (gate_up + silu*up, M=2048)", "mfma",
+                                    flops / secs / 1e12, flops, secs)
     if not args.no_cpu_baseline:
         from oracle import model as om
         from oracle.attention import build_attention_metadata as oracle_meta
