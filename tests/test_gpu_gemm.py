@@ -190,3 +190,27 @@ def test_gemm_qk_norm_rope_cache_matches_unfused(m, heads, kv_heads, k):
     kn = ol.rms_norm(ref[:, heads * d : (heads + kv_heads) * d].reshape(m, kv_heads, d), nk, 1e-6)
     qo, _ = ol.apply_rope(qn, kn, cos_t[pos], sin_t[pos])
     assert rel_l2(q1.cpu(), qo) < 1e-2
+
+
+@pytest.mark.parametrize("m,n,k", [(300, 1000, 1024), (2048, 5120, 1024)])
+@pytest.mark.parametrize("epilogue", [0, 1, 2])
+def test_gemm_unaligned_output_rows(m, n, k, epilogue):
+    """Output (and residual) rows whose stride is not a multiple of 8 elements take the kernels'
+    element-by-element stores; the values match the aligned call bit for bit (the 128 x 128 tiling
+    at 300 tokens, the 256 x 256 one at 2048)."""
+    q, s = oi.quantize_int8(_bf16((n, k), seed=n + k + 5, std=0.02))
+    x = _bf16((m, k), seed=m + 13)
+    xd, qd, sd = x.to(DEV), q.to(DEV), s.to(DEV)
+    cols = n // 2 if epilogue == 1 else n
+    r = _bf16((m, n), seed=m + 14).to(DEV)
+
+    def run(pad):
+        y = torch.zeros(m, cols + pad, dtype=torch.bfloat16, device=DEV)
+        rr = torch.zeros(m, n + pad, dtype=torch.bfloat16, device=DEV)
+        rr[:, :n] = r
+        _native.call("msa_int8_gemm", kernels._ptr(xd), m, k, k, kernels._ptr(qd), kernels._ptr(sd), n,
+                     kernels._ptr(y), cols + pad, epilogue, kernels._ptr(rr) if epilogue == 2 else None,
+                     n + pad if epilogue == 2 else 0, kernels._stream(y))
+        return y[:, :cols].cpu()
+
+    assert torch.equal(run(0), run(3))
