@@ -30,7 +30,6 @@ from torch import Tensor
 from miniserve_amd.attention.backends import AttentionMetadata, DecodePlan, SeqChunk, build_attention_metadata
 from miniserve_amd.model.qwen3 import Qwen3ForCausalLM
 from miniserve_amd.runner.sampler import sample
-from miniserve_amd.utils import to_device
 
 
 @dataclass
@@ -171,30 +170,44 @@ class ModelRunner:
         self.graphs = {}  # captured graphs hold the old pool's addresses
 
     def prepare(self, scheduled: list[ScheduledChunk]) -> StepInputs:
-        """Flatten all scheduled tokens into one batch (model_runner.py:162-205, no speculation)."""
+        """Flatten all scheduled tokens into one batch (model_runner.py:162-205, no speculation).
+
+        Ids, positions, slots and sampled rows are built in one int64 host array (a chunk's slots
+        vectorized through its block table) and uploaded with one pinned, non-blocking copy."""
         bs = self.block_size
-        input_ids: list[int] = []
-        positions: list[int] = []
-        slots: list[int] = []
+        total = sum(s.num_new for s in scheduled)
         chunks: list[SeqChunk] = []
         rows: list[int] = []
         sample_idx: list[int] = []
+        buf = np.empty(3 * total + len(scheduled), dtype=np.int64)
+        ids, pos, slt = buf[:total], buf[total : 2 * total], buf[2 * total : 3 * total]
+        flat = 0
         for idx, s in enumerate(scheduled):
             start, n, table = s.num_computed, s.num_new, s.block_table
-            flat = len(input_ids)
-            input_ids.extend(s.token_ids[start : start + n])
-            positions.extend(range(start, start + n))
-            slots.extend(table[p // bs] * bs + p % bs for p in range(start, start + n))
+            if n == 1:
+                ids[flat] = s.token_ids[start]
+                pos[flat] = start
+                slt[flat] = table[start // bs] * bs + start % bs
+            elif n > 1:
+                p = np.arange(start, start + n, dtype=np.int64)
+                ids[flat : flat + n] = s.token_ids[start : start + n]
+                pos[flat : flat + n] = p
+                tab = np.asarray(table[: (start + n - 1) // bs + 1], dtype=np.int64)
+                slt[flat : flat + n] = tab[p // bs] * bs + p % bs
             chunks.append(SeqChunk(flat, n, start, table))
             if start + n == len(s.token_ids):
                 sample_idx.append(idx)
                 rows.append(flat + n - 1)
-        slot_mapping = to_device(slots, self.device)
+            flat += n
+        buf[3 * total : 3 * total + len(rows)] = rows
+        host = torch.from_numpy(buf[: 3 * total + len(rows)])
+        dev = host.to(self.device) if self.device.type != "cuda" else host.pin_memory().to(self.device, non_blocking=True)
+        slot_mapping = dev[2 * total : 3 * total]
         return StepInputs(
-            input_ids=to_device(input_ids, self.device),
-            positions=to_device(positions, self.device),
+            input_ids=dev[:total],
+            positions=dev[total : 2 * total],
             attn=build_attention_metadata(chunks, slot_mapping, bs),
-            logits_rows=to_device(rows, self.device),
+            logits_rows=dev[3 * total :],
             sample_idx=sample_idx,
         )
 
