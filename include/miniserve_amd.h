@@ -288,13 +288,16 @@ int msa_paged_attention_decode_qkv(const uint16_t* qkv, int64_t ldqkv, const uin
  * steps as msa_qk_norm_rope_cache, bit for bit: q_out [m, heads, 128] gets the normed, rotated
  * queries, k_cache / v_cache [num_slots, kv_heads, 128] the normed, rotated keys and the values at
  * slot_mapping[t] (slots outside [0, num_slots) are skipped). cos / sin are [m, 128] float32.
- * head_dim must be 128; x, the norm weights, cos / sin, q_out and the caches 16-byte aligned. */
+ * head_dim must be 128; x, the norm weights, cos / sin, q_out and the caches 16-byte aligned.
+ * When the GEMM would split K (few output tiles) and the workspace holds
+ * msa_int8_linear_workspace_size(m, n, k) bytes, the split-K partials go to the workspace and
+ * msa_qk_norm_rope_cache_splitk sums them (the same values); otherwise the epilogue does it. */
 int msa_int8_gemm_qk_norm_rope_cache(const uint16_t* x, int64_t m, int64_t k, int64_t ldx, const int8_t* qweight,
                                      const uint16_t* scale, int heads, int kv_heads, int head_dim,
                                      const uint16_t* q_norm_w, const uint16_t* k_norm_w, float eps,
                                      const float* cos, const float* sin, const int64_t* slot_mapping,
                                      uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache, int64_t num_slots,
-                                     msa_stream_t stream);
+                                     void* workspace, size_t workspace_bytes, msa_stream_t stream);
 
 /* The prefill path of paged_attention (attention/backends.py:182-196) for chunks of any length,
  * fresh or continuing from cached keys: causal attention of each new token over positions

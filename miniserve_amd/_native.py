@@ -127,7 +127,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "msa_int8_gemm_qk_norm_rope_cache": (
         c_int,
         [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p, c_void_p, c_float,
-         c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p],
+         c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_size_t, c_void_p],
     ),
     "msa_paged_attention_prefill": (
         c_int,

@@ -681,7 +681,8 @@ extern "C" int msa_int8_gemm_qk_norm_rope_cache(const uint16_t* x, int64_t m, in
                                                int head_dim, const uint16_t* q_norm_w, const uint16_t* k_norm_w,
                                                float eps, const float* cos, const float* sin,
                                                const int64_t* slot_mapping, uint16_t* q_out, uint16_t* k_cache,
-                                               uint16_t* v_cache, int64_t num_slots, msa_stream_t stream) {
+                                               uint16_t* v_cache, int64_t num_slots, void* workspace,
+                                               size_t workspace_bytes, msa_stream_t stream) {
   const char* who = "msa_int8_gemm_qk_norm_rope_cache";
   if (m == 0) return MSA_OK;
   if (!x || !qweight || !scale || !q_norm_w || !k_norm_w || !cos || !sin || !slot_mapping || !q_out || !k_cache ||
@@ -697,6 +698,17 @@ extern "C" int msa_int8_gemm_qk_norm_rope_cache(const uint16_t* x, int64_t m, in
       !aligned16(k_cache) || !aligned16(v_cache))
     return fail(MSA_ERR_INVALID, std::string(who) + ": norm weights, cos / sin, q_out and caches must be 16-byte aligned");
   const int64_t n = (int64_t)(heads + 2 * kv_heads) * 128;
+  // Few output tiles: split-K partials into the workspace, then the q/k-norm kernel that sums them
+  // (the same values: partials summed in split order, rounded to bf16, then normed).
+  const int splits = gemm_splits(m, n, k, MSA_EPI_NONE);
+  if (splits > 1 && workspace && workspace_bytes >= gemm_workspace_size(m, n, k, MSA_EPI_NONE) && aligned16(workspace)) {
+    const int got = gemm_run_partials(x, m, k, ldx, qweight, scale, n, (float*)workspace, workspace_bytes,
+                                      (hipStream_t)stream);
+    if (got < 0) return check_launch(who);
+    if (got > 1)
+      return msa_qk_norm_rope_cache_splitk((const float*)workspace, got, m, heads, kv_heads, 128, q_norm_w, k_norm_w,
+                                           eps, cos, sin, slot_mapping, q_out, k_cache, v_cache, num_slots, stream);
+  }
   GemmArgs a{};
   a.x = x; a.ldx = ldx; a.w = qweight; a.scale = scale;
   a.m = (int)m; a.n = (int)n; a.k = (int)k;

@@ -296,11 +296,10 @@ def qk_norm_rope_cache(
 
 
 def qkv_gemm_fuses_norm(m: int, heads: int, kv_heads: int, head_dim: int, k: int) -> bool:
-    """Whether the qkv projection of ``m`` tokens takes the unsplit prefill GEMM, whose epilogue can
-    apply the q/k-norm, RoPE and cache write (``int8_linear_qk_norm_rope_cache``)."""
-    n = (heads + 2 * kv_heads) * head_dim
-    return (head_dim == 128 and m >= 128 and k % 64 == 0
-            and _native.query("msa_int8_linear_workspace_size", m, n, k) == 0)
+    """Whether the qkv projection of ``m`` tokens takes the prefill GEMM with the q/k-norm, RoPE and
+    cache write fused after it (``int8_linear_qk_norm_rope_cache``): in its epilogue, or in the
+    kernel that merges its split-K partials."""
+    return head_dim == 128 and m >= 128 and k % 64 == 0
 
 
 def int8_linear_qk_norm_rope_cache(
@@ -333,10 +332,12 @@ def int8_linear_qk_norm_rope_cache(
     _check(k_cache.is_contiguous() and v_cache.is_contiguous() and k_cache.shape == v_cache.shape, "caches")
     _check(k_cache.shape[-2:] == (kv_heads, head_dim), "cache layout [slots, KVH, D]")
     q = torch.empty(t, heads, head_dim, dtype=torch.bfloat16, device=x.device)
+    ws_bytes = _native.query("msa_int8_linear_workspace_size", t, qweight.shape[0], k) if t else 0
+    ws = workspaces.get("linear", x.device, ws_bytes)
     _native.call(
         "msa_int8_gemm_qk_norm_rope_cache", _ptr(x), t, k, x.stride(0), _ptr(qweight), _ptr(scale), heads, kv_heads,
         head_dim, _ptr(q_norm_w), _ptr(k_norm_w), float(eps), _ptr(cos), _ptr(sin), _ptr(slot_mapping), _ptr(q),
-        _ptr(k_cache), _ptr(v_cache), k_cache.shape[0], _stream(x),
+        _ptr(k_cache), _ptr(v_cache), k_cache.shape[0], _ptr(ws), ws.numel() if ws is not None else 0, _stream(x),
     )
     return q
 

@@ -156,10 +156,11 @@ def test_linear_add_rmsnorm(m, n, k):
 
 @pytest.mark.parametrize("m,heads,kv_heads,k", [(2048, 16, 8, 1024), (300, 32, 8, 1024), (129, 8, 8, 2048)])
 def test_gemm_qk_norm_rope_cache_matches_unfused(m, heads, kv_heads, k):
-    """The qkv GEMM with the q/k-norm + RoPE + cache write in its epilogue against the unsplit GEMM
-    followed by the standalone kernel (pinned against the oracle in test_gpu_kernels.py): the same
-    q and caches bit for bit, including skipped slots (-1 and past the pool); and q within the
-    oracle's bar."""
+    """The qkv GEMM with the q/k-norm + RoPE + cache write fused after it (in its epilogue at 2048
+    tokens; split-K partials summed by the q/k-norm kernel at 300 and 129, where the GEMM splits)
+    against the plain linear on the same route followed by the standalone kernel (pinned against
+    the oracle in test_gpu_kernels.py): the same q and caches bit for bit, including skipped slots
+    (-1 and past the pool); and q within the oracle's bar."""
     d = 128
     n = (heads + 2 * kv_heads) * d
     qw8, sc = oi.quantize_int8(_bf16((n, k), seed=m + heads, std=0.02))
@@ -177,10 +178,10 @@ def test_gemm_qk_norm_rope_cache_matches_unfused(m, heads, kv_heads, k):
     args = (nq.to(DEV), nk.to(DEV), 1e-6, cos_t[pos].contiguous().to(DEV), sin_t[pos].contiguous().to(DEV), slots.to(DEV))
     kc1 = torch.zeros(num_slots, kv_heads, d, dtype=torch.bfloat16, device=DEV)
     vc1, kc2, vc2 = torch.zeros_like(kc1), torch.zeros_like(kc1), torch.zeros_like(kc1)
+    splits = _native.query("msa_int8_linear_workspace_size", m, n, k) > 0
+    assert splits == (m < 2048)
     q1 = kernels.int8_linear_qk_norm_rope_cache(xd, qd, sd, heads, kv_heads, d, *args, kc1, vc1)
-    qkv = torch.empty(m, n, dtype=torch.bfloat16, device=DEV)
-    _native.call("msa_int8_gemm", kernels._ptr(xd), m, k, k, kernels._ptr(qd), kernels._ptr(sd), n, kernels._ptr(qkv),
-                 n, 0, None, 0, kernels._stream(qkv))  # unsplit
+    qkv = kernels.int8_linear(xd, qd, sd)  # the same GEMM route (128 x 128 tiles, split or not)
     q2 = kernels.qk_norm_rope_cache(qkv, heads, kv_heads, d, *args, kc2, vc2)
     assert torch.equal(q1, q2)
     assert torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
