@@ -63,7 +63,6 @@ __global__ __launch_bounds__(256) void int8_gemm256_kernel(BigGemmArgs a) {
   uint16_t* As = bsm;                   // [2][256][kBLd]
   uint16_t* Bs = bsm + 2 * kBM * kBLd;  // [2][256][kBLd]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int j = lane & 15, g = lane >> 4;
   const int wm = wave >> 1, wn = wave & 1;
   // XCD-aware order: the token blocks of one weight block run on one XCD (round-robin dispatch),
   // so its weight tiles come from HBM once and from that XCD's L2 after.
@@ -76,8 +75,8 @@ __global__ __launch_bounds__(256) void int8_gemm256_kernel(BigGemmArgs a) {
   // (i < 4), 16-byte chunk tid % 4.
   const int ar = tid >> 3, ac = (tid & 7) * 8;
   const int br = tid >> 2, bc = (tid & 3) * 16;
-  // 32-bit byte offsets from the uniform base pointers (the caller checks that they fit), so each
-  // global load takes a scalar base plus one vector register.
+  // 32-bit byte offsets from the uniform base pointers (the caller checks that they fit): half the
+  // registers of per-row 64-bit pointers.
   uint32_t aoff[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
