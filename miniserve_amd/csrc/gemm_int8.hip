@@ -74,7 +74,6 @@ __global__ __launch_bounds__(256) void int8_gemm_kernel(GemmArgs a) {
   uint16_t* As = gsm;                    // [2][128][kGLd]
   uint16_t* Bs = gsm + 2 * kGBM * kGLd;  // [2][128][kGLd]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int j = lane & 15, g = lane >> 4;
   const int wm = wave >> 1, wn = wave & 1;
   const int nb = blockIdx.x % a.n_blocks, rest = blockIdx.x / a.n_blocks;
   const int mb = rest % a.m_blocks, ks = rest / a.m_blocks;  // ks: the split of K (0 without split-K)
@@ -127,25 +126,28 @@ __global__ __launch_bounds__(256) void int8_gemm_kernel(GemmArgs a) {
     *(bf16x8*)(B_ + 64 * kGLd + 8) = dequant8(p##b1.z, p##b1.w, bs[1]);     \
   } while (0)
 
-  f32x4 acc[4][4];
+  // 32 x 32 x 16 MFMAs, 2 x 2 tiles per wavefront: lane (h, r) holds row r of a 32-row operand
+  // tile, K elements 8h..8h+7 of each 16-wide slice.
+  const int r32 = lane & 31, h = lane >> 5;
+  f32x16 acc[2][2];
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
+  for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = f32x16{};
 
 #define MSA_GEMM_COMPUTE(cur)                                                                        \
   do {                                                                                               \
-    const uint16_t* A = As + (cur) * kGBM * kGLd + (wm * 64 + j) * kGLd + g * 8;                      \
-    const uint16_t* B = Bs + (cur) * kGBN * kGLd + (wn * 64 + j) * kGLd + g * 8;                      \
-    _Pragma("unroll") for (int ks = 0; ks < 2; ++ks) {                                               \
-      bf16x8 af[4], bfr[4];                                                                          \
-      _Pragma("unroll") for (int t = 0; t < 4; ++t) {                                                \
-        af[t] = *(const bf16x8*)(A + t * 16 * kGLd + ks * 32);                                       \
-        bfr[t] = *(const bf16x8*)(B + t * 16 * kGLd + ks * 32);                                      \
+    const uint16_t* A = As + (cur) * kGBM * kGLd + (wm * 64 + r32) * kGLd + h * 8;                    \
+    const uint16_t* B = Bs + (cur) * kGBN * kGLd + (wn * 64 + r32) * kGLd + h * 8;                    \
+    _Pragma("unroll") for (int ks = 0; ks < 4; ++ks) {                                               \
+      bf16x8 af[2], bfr[2];                                                                          \
+      _Pragma("unroll") for (int t = 0; t < 2; ++t) {                                                \
+        af[t] = *(const bf16x8*)(A + t * 32 * kGLd + ks * 16);                                       \
+        bfr[t] = *(const bf16x8*)(B + t * 32 * kGLd + ks * 16);                                      \
       }                                                                                              \
-      _Pragma("unroll") for (int mt = 0; mt < 4; ++mt)                                               \
-        _Pragma("unroll") for (int nt = 0; nt < 4; ++nt)                                             \
-          acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt], bfr[nt], acc[mt][nt], 0, 0, 0); \
+      _Pragma("unroll") for (int mt = 0; mt < 2; ++mt)                                               \
+        _Pragma("unroll") for (int nt = 0; nt < 2; ++nt)                                             \
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mt], bfr[nt], acc[mt][nt], 0, 0, 0); \
     }                                                                                                \
   } while (0)
 
@@ -174,18 +176,19 @@ __global__ __launch_bounds__(256) void int8_gemm_kernel(GemmArgs a) {
 #undef MSA_GEMM_STORE
 #undef MSA_GEMM_COMPUTE
 
-  // lane (g, j) of tile (mt, nt): tokens m0 + wm*64 + mt*16 + 4g + i, LDS weight row wn*64 + nt*16 + j
+  // value i of lane (h, r) in tile (mt, nt): token m0 + wm*64 + mt*32 + 8(i/4) + 4h + i%4, LDS
+  // weight row wn*64 + nt*32 + r
   if constexpr (EPI == kEpiPartial) {
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
+    for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int tok = m0 + wm * 64 + mt * 16 + 4 * g + i;
+      for (int i = 0; i < 16; ++i) {
+        const int tok = m0 + wm * 64 + mt * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
         if (tok >= a.m) continue;
         float* prow = a.part + ((int64_t)ks * a.m + tok) * a.n;
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt) {
-          const int col = nb * kGBN + wn * 64 + nt * 16 + j;
+        for (int nt = 0; nt < 2; ++nt) {
+          const int col = nb * kGBN + wn * 64 + nt * 32 + r32;
           if (col < a.n) prow[col] = acc[mt][nt][i];
         }
       }
@@ -196,19 +199,17 @@ __global__ __launch_bounds__(256) void int8_gemm_kernel(GemmArgs a) {
     uint16_t* Cs = gsm;  // [128 tokens][kCLd]
     __syncthreads();
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
+    for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        uint16_t* c = Cs + (wm * 64 + mt * 16 + 4 * g + i) * kCLd + j;
+      for (int i = 0; i < 16; ++i) {
+        uint16_t* c = Cs + (wm * 64 + mt * 32 + 8 * (i >> 2) + 4 * h + (i & 3)) * kCLd + r32;
         if constexpr (EPI == MSA_EPI_SILU_MUL) {
-#pragma unroll
-          for (int nt = 0; nt < 2; ++nt) {
-            const float gt = round_bf16(acc[mt][nt][i]), up = round_bf16(acc[mt][nt + 2][i]);
-            c[wn * 32 + nt * 16] = f32_to_bf16(round_bf16(silu_f32(gt)) * up);
-          }
+          // the wavefront's 64 weight rows: 32 gate rows (tile 0), then their 32 up rows (tile 1)
+          const float gt = round_bf16(acc[mt][0][i]), up = round_bf16(acc[mt][1][i]);
+          c[wn * 32] = f32_to_bf16(round_bf16(silu_f32(gt)) * up);
         } else {
 #pragma unroll
-          for (int nt = 0; nt < 4; ++nt) c[wn * 64 + nt * 16] = f32_to_bf16(acc[mt][nt][i]);
+          for (int nt = 0; nt < 2; ++nt) c[wn * 64 + nt * 32] = f32_to_bf16(acc[mt][nt][i]);
         }
       }
     __syncthreads();
