@@ -333,6 +333,11 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __
 // K splits of the GEMM: 1 when the output tiles fill the GPU (or for silu * up), else the fewest
 // splits (of whole 64-wide steps, at least 512 of K each, at most 8) that give 256+ workgroups,
 // or the most such splits when none does.
+// Workgroups a split-K launch aims for (splits are added until the tiles times the splits reach it).
+#ifndef MSA_SPLITK_TARGET_WGS
+#define MSA_SPLITK_TARGET_WGS 256
+#endif
+
 int gemm_splits(int64_t m, int64_t n, int64_t k, int epilogue) {
   if (epilogue == MSA_EPI_SILU_MUL || k % kGBK != 0) return 1;
   const int64_t tiles = ((n + kGBN - 1) / kGBN) * ((m + kGBM - 1) / kGBM);
@@ -342,7 +347,7 @@ int gemm_splits(int64_t m, int64_t n, int64_t k, int epilogue) {
   for (int s = 2; s <= 8; ++s) {
     if (steps % s != 0 || k / s < 512) continue;
     best = s;
-    if (tiles * s >= 256) break;
+    if (tiles * s >= MSA_SPLITK_TARGET_WGS) break;
   }
   return best;
 }
