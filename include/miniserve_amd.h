@@ -283,7 +283,7 @@ int msa_paged_attention_decode_qkv(const uint16_t* qkv, int64_t ldqkv, const uin
 /* The qkv projection of a prefill-sized batch with the per-head q/k RMSNorm, RoPE and KV-cache
  * write of msa_qk_norm_rope_cache in its epilogue (model/qwen3.py:94-98, then the cache write of
  * attention/backends.py:159-160): y = x @ bf16(q * s)^T as msa_int8_gemm computes it
- * (float32 sums rounded to bf16, never split over K), n = (heads + 2 kv_heads) * 128 weight rows
+ * (float32 sums rounded to bf16), n = (heads + 2 kv_heads) * 128 weight rows
  * whose 128-row blocks are the head slots (q heads, k heads, v heads); then the same rounding
  * steps as msa_qk_norm_rope_cache, bit for bit: q_out [m, heads, 128] gets the normed, rotated
  * queries, k_cache / v_cache [num_slots, kv_heads, 128] the normed, rotated keys and the values at
