@@ -188,11 +188,8 @@ __global__ __launch_bounds__(64 * W) void paged_decode_kernel(DecodeArgs a) {
     for (int rr = 0; rr < 2; ++rr)
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
-        // read once: non-temporal, so the stream of keys and values does not evict what is reused
-        const u32x4 kx = __builtin_nontemporal_load((const u32x4*)(a.kc + base + rr * rs + hf * hs));
-        const u32x4 vx = __builtin_nontemporal_load((const u32x4*)(a.vc + base + rr * rs + hf * hs));
-        kr[rr][hf] = uint4{kx.x, kx.y, kx.z, kx.w};
-        vr[rr][hf] = uint4{vx.x, vx.y, vx.z, vx.w};
+        kr[rr][hf] = load_once16(a.kc + base + rr * rs + hf * hs);
+        vr[rr][hf] = load_once16(a.vc + base + rr * rs + hf * hs);
       }
   };
   uint4 ka[2][2], va[2][2], kb[2][2], vb[2][2];

@@ -41,6 +41,13 @@ __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to
 __device__ __forceinline__ float silu_f32(float x) {
   return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * kLog2e));
 }
+// A 16-byte load of data read once per step (the KV cache read by decode attention):
+// non-temporal, so the stream does not evict what is reused.
+__device__ __forceinline__ uint4 load_once16(const void* p) {
+  const u32x4 v = __builtin_nontemporal_load((const u32x4*)p);
+  return uint4{v.x, v.y, v.z, v.w};
+}
+
 // Per-head RMSNorm then RoPE of one 128-dim head row (model/layers.py:18-22, 56-65 rounding: y =
 // bf16(w * bf16(x * r)), out = bf16(y0 * c) + bf16(-y1 * s), bf16(y1 * c) + bf16(y0 * s), each
 // product rounded, the sum rounded by the caller's store) held by eight consecutive lanes: lane
