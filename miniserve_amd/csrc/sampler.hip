@@ -586,7 +586,7 @@ __global__ __launch_bounds__(kCandThreads) void sample_chunk_kernel(CandArgs c) 
   // would wait for what was issued before it.
   float vals[kCandPerThread];
 #pragma unroll
-  for (int i = 0; i < kCandPerThread; ++i) vals[i] = lg[min(i * kCandThreads + tid, n - 1)];
+  for (int i = 0; i < kCandPerThread; ++i) vals[i] = __builtin_nontemporal_load(lg + min(i * kCandThreads + tid, n - 1));
   if (a.greedy && a.greedy[row]) {  // first index of the largest raw logit in the chunk
     float bv = -INFINITY;
     int bi = 0x7fffffff;
