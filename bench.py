@@ -43,9 +43,9 @@ HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 BATCH, CTX_LO, CTX_HI = 64, 256, 384
 # FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 of one fused decode-attention launch on the decode workload,
-# from rocprofv3 --pmc: 42,902.07 KiB x 2 x 1024 + 512 KiB x 1024
+# from rocprofv3 --pmc: 42,870.85 KiB x 2 x 1024 + 512 KiB x 1024
 # (profiles/paged_decode_kernel_traffic_pmc.md).
-ATTN_TRAFFIC_BYTES: int | None = 88_321_135
+ATTN_TRAFFIC_BYTES: int | None = 88_323_789
 # The same counters over one layer's four decode linears, summed (profiles/dec_linear_kernel_pmc.md).
 LINEAR_TRAFFIC_BYTES: int | None = 25_925_165
 
